@@ -1,0 +1,180 @@
+"""KV-cache producers: RoPE, append, fused rotate+append, growth, Q8_0.
+
+Mirrors crates/llmtie-cuda/tests/kernels.rs:1443-1539 (rope at every offset,
+Llama-3 factors, no-divisor bit equality), :1919-2069 (the fused rotate+cache
+is the chain), :2144-2240 (growth re-strides every head; refusals). The Q8_0
+producers have no reference test; they are held to ggml's quantizer (oracle)
+bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.util import down, full_scale_err, up, up_f16
+
+pytestmark = pytest.mark.gpu
+
+F32EPS = float(np.finfo(np.float32).eps)
+LLAMA3_DIV = np.array([1.0] * 29 + [1.207484, 1.553415, 2.026313, 2.69453, 3.684253, 5.257327] + [8.0] * 29,
+                      np.float32)
+
+
+@pytest.mark.parametrize("first", [0, 1, 17, 4095])
+def test_rope_matches_at_every_offset(gpu, first):
+    t, heads, hd = 5, 3, 128
+    x = oracle.seq(t * heads * hd, 75)
+    want = oracle.rope(x, t, heads, hd, 10000.0, first)
+    dev = up(x)
+    gpu.rope(dev, 0, t, heads, hd, 10000.0, first)
+    assert full_scale_err(want, down(dev)) < 1e-5 + first * F32EPS
+
+
+@pytest.mark.parametrize("first", [0, 1, 4095])
+def test_scaled_rope_matches_the_twin_with_llama3_factors(gpu, first):
+    t, heads, hd = 4, 3, 128
+    x = oracle.seq(t * heads * hd, 91)
+    want = oracle.rope(x, t, heads, hd, 500000.0, first, LLAMA3_DIV)
+    dev = up(x)
+    gpu.rope_scaled(dev, 0, up(LLAMA3_DIV), t, heads, hd, 500000.0, first)
+    assert full_scale_err(want, down(dev)) < 1e-5 + first * F32EPS
+
+
+def test_scaled_rope_with_no_divisor_is_the_unscaled_one(gpu):
+    t, heads, hd = 3, 2, 64
+    x = oracle.seq(t * heads * hd, 12)
+    a, b = up(x), up(x)
+    gpu.rope(a, 0, t, heads, hd, 10000.0, 7)
+    gpu.rope_scaled(b, 0, None, t, heads, hd, 10000.0, 7)
+    assert np.array_equal(down(a), down(b))
+
+
+@pytest.mark.parametrize("pos,scaled", [(0, True), (7, False), (31, True)])
+def test_the_fused_rotate_and_cache_is_the_chain_it_replaces(gpu, pos, scaled):
+    heads, kv, hd, cap = 6, 2, 16, 32
+    half = hd // 2
+    div = np.array([1.0 if i < 5 else 8.0 for i in range(half)], np.float32)
+    theta = 500000.0
+    qk = oracle.seq(heads * hd + kv * hd + 5, 17)
+    vv = oracle.seq(kv * hd + 3, 23)
+    q_off, k_off, v_off = 0, heads * hd + 5, 3
+    kfill = oracle.seq(cap * kv * hd, 5)
+    vfill = oracle.seq(cap * kv * hd, 9)
+    d = up(div) if scaled else None
+    # The chain: two rotations, two appends.
+    cqk, cv = up(qk), up(vv)
+    ck, cvc = up_f16(kfill), up_f16(vfill)
+    gpu.rope_scaled(cqk, q_off, d, 1, heads, hd, theta, pos)
+    gpu.rope_scaled(cqk, k_off, d, 1, kv, hd, theta, pos)
+    gpu.cache_append_f16(cqk, k_off, ck, 1, kv, hd, cap, pos, False)
+    gpu.cache_append_f16(cv, v_off, cvc, 1, kv, hd, cap, pos, True)
+    # The fused kernel.
+    fqk, fv = up(qk), up(vv)
+    fk, fvc = up_f16(kfill), up_f16(vfill)
+    gpu.rope_cache_f16(fqk, q_off, fqk, k_off, fv, v_off, d, heads, kv, hd, theta, pos, fk, fvc, cap)
+    assert np.array_equal(down(cqk)[:heads * hd], down(fqk)[:heads * hd]), "q"
+    assert np.array_equal(down(ck).view(np.uint16), down(fk).view(np.uint16)), "k cache"
+    assert np.array_equal(down(cvc).view(np.uint16), down(fvc).view(np.uint16)), "v cache"
+    # And the cache holds what the oracle's rotation rounds to.
+    want_q = oracle.rope(qk[:heads * hd], 1, heads, hd, theta, pos, div if scaled else None)
+    assert full_scale_err(want_q, down(fqk)[:heads * hd]) < 1e-5 + pos * F32EPS
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+def test_growing_a_cache_puts_every_head_where_the_larger_capacity_wants_it(gpu, transposed):
+    live, kv, hd, small, large = 5, 3, 4, 8, 16
+    src = up(oracle.seq(live * kv * hd, 7))
+    for f16 in (False, True):
+        mk = (lambda n: torch.zeros(n, dtype=torch.float16, device="cuda")) if f16 else \
+             (lambda n: torch.zeros(n, device="cuda"))
+        app = gpu.cache_append_f16 if f16 else gpu.cache_append
+        grow = gpu.cache_grow_f16 if f16 else gpu.cache_grow
+        grew = mk(small * kv * hd)
+        app(src, 0, grew, live, kv, hd, small, 0, transposed)
+        moved = mk(large * kv * hd)
+        grow(grew, moved, kv, hd, small, large, live, transposed)
+        direct = mk(large * kv * hd)
+        app(src, 0, direct, live, kv, hd, large, 0, transposed)
+        assert torch.equal(moved, direct)
+
+
+def test_a_growth_that_shrinks_or_overruns_is_refused(gpu):
+    from ttsxabe_amd.gpu import CacheOverrun
+    kv, hd, small, large = 2, 4, 8, 16
+    src = torch.zeros(small * kv * hd, device="cuda")
+    dst = torch.zeros(large * kv * hd, device="cuda")
+    with pytest.raises(CacheOverrun):
+        gpu.cache_grow(src, dst, kv, hd, small, large, small + 1, False)
+    smaller = torch.zeros(small * kv * hd, device="cuda")
+    with pytest.raises(CacheOverrun):
+        gpu.cache_grow(src, smaller, kv, hd, large, small, 4, False)
+
+
+def test_an_offset_past_the_end_of_the_source_is_refused(gpu):
+    from ttsxabe_amd.gpu import SliceOverrun
+    t, heads, hd = 2, 2, 8
+    x = torch.zeros(t * heads * hd, device="cuda")
+    with pytest.raises(SliceOverrun):
+        gpu.rope(x, 1, t, heads, hd, 10000.0, 0)
+    dst = torch.zeros(8 * heads * hd, device="cuda")
+    with pytest.raises(SliceOverrun):
+        gpu.cache_append(x, 1, dst, t, heads, hd, 8, 0, False)
+
+
+def _q8_views(cache):
+    kc = down(cache.k_codes)
+    vc = down(cache.v_codes)
+    ks = down(cache.k_scales).view(np.uint16)
+    vs = down(cache.v_scales).view(np.uint16)
+    return kc, ks, vc, vs
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_q8_append_is_ggml_quantize(gpu, hd):
+    from ttsxabe_amd.gpu import KvCacheQ8
+    slots, kv, cap, n, past, slot = 3, 2, 64, 9, 5, 1
+    cache = KvCacheQ8(slots, kv, hd, cap)
+    k = oracle.seq(n * kv * hd, 401) * np.float32(3.0)
+    v = oracle.seq(n * kv * hd, 402)
+    k[:32] = 0.0  # an all-zero block: scale 0, codes 0
+    v[5] = 127.0 * 0.5 / 10.0  # a value sitting near a rounding tie
+    gpu.kv_q8_append(up(k), 0, up(v), 0, cache, slot, n, past)
+    kc, ks, vc, vs = _q8_views(cache)
+    nb = hd // 32
+    for t in range(n):
+        for h in range(kv):
+            row = (t * kv + h) * hd
+            wc, wsc = oracle.q8_0_quantize(k[row:row + hd])
+            kvh = slot * kv + h
+            at = (kvh * cap + past + t)
+            assert np.array_equal(kc[at * hd:(at + 1) * hd], wc)
+            assert np.array_equal(ks[at * nb:(at + 1) * nb], wsc)
+            wc, wsc = oracle.q8_0_quantize(v[row:row + hd])
+            got = vc.reshape(slots * kv, hd, cap)[kvh, :, past + t]
+            assert np.array_equal(got, wc)
+            assert np.array_equal(vs[at * nb:(at + 1) * nb], wsc)
+    # Nothing outside the written positions moved.
+    mask = np.zeros((slots * kv, cap), bool)
+    mask[slot * kv:(slot + 1) * kv, past:past + n] = True
+    assert (kc.reshape(slots * kv, cap, hd)[~mask] == 0).all()
+
+
+def test_the_q8_rotate_and_cache_is_rope_then_q8_append(gpu):
+    from ttsxabe_amd.gpu import KvCacheQ8
+    heads, kv, hd, cap, slots, slot, pos = 8, 2, 128, 64, 2, 1, 37
+    theta = 500000.0
+    q = oracle.seq(heads * hd, 31)
+    k = oracle.seq(kv * hd, 32)
+    v = oracle.seq(kv * hd, 33)
+    div = up(LLAMA3_DIV)
+    a = KvCacheQ8(slots, kv, hd, cap)
+    qa, ka = up(q), up(k)
+    gpu.rope_scaled(qa, 0, div, 1, heads, hd, theta, pos)
+    gpu.rope_scaled(ka, 0, div, 1, kv, hd, theta, pos)
+    gpu.kv_q8_append(ka, 0, up(v), 0, a, slot, 1, pos)
+    b = KvCacheQ8(slots, kv, hd, cap)
+    qb = up(q)
+    gpu.rope_cache_q8(qb, 0, up(k), 0, up(v), 0, div, heads, theta, pos, b, slot)
+    assert torch.equal(qa, qb)
+    for x, y in zip(_q8_views(a), _q8_views(b)):
+        assert np.array_equal(x, y)

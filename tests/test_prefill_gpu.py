@@ -1,0 +1,107 @@
+"""Prefill (flash) attention against the reference's f64 prefill reference.
+
+Mirrors crates/llmtie-cuda/tests/kernels.rs:2242-2473 (`fused_attention_sized`
+and its callers): q = seq * 100 so softmax rows are peaked, K/V from `seq`,
+the caches' own layouts with unused capacity zeroed, tolerance
+2e-4 + 1e-2|want| + 1e-2*spread per element and worst/tol < 0.5. Plus the
+f16-vs-f32 cache agreement (:2561-2731) and the rows mode's bit equality with
+the split path (:4040-4081).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.util import down, up, up_f16
+
+pytestmark = pytest.mark.gpu
+
+
+def caches(kvals, vvals, kv, tk, cap, hd):
+    kc = np.zeros(kv * cap * hd, np.float32)
+    vc = np.zeros(kv * hd * cap, np.float32)
+    kvr = kvals.reshape(kv, tk, hd)
+    vvr = vvals.reshape(kv, tk, hd)
+    kc.reshape(kv, cap, hd)[:, :tk, :] = kvr
+    vc.reshape(kv, hd, cap)[:, :, :tk] = vvr.transpose(0, 2, 1)
+    return kc, vc
+
+
+def fused_attention_sized(gpu, heads, kv, hd, causal, tq, past, cap, half):
+    tk = past + tq
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    q = oracle.seq(tq * heads * hd, 71) * np.float32(100.0)
+    kc, vc = caches(oracle.seq(kv * tk * hd, 72), oracle.seq(kv * tk * hd, 73), kv, tk, cap, hd)
+    if half:
+        out = gpu.flash_attn_f16(up(q), up_f16(kc), up_f16(vc), tq, past, heads, kv, hd, cap, scale, causal)
+    else:
+        out = gpu.flash_attn(up(q), up(kc), up(vc), tq, past, heads, kv, hd, cap, scale, causal)
+    got = down(out).astype(np.float64)
+    want, spread = oracle.prefill_ref(q, heads * hd, kc, vc, tq, past, heads, kv, hd, cap, scale, causal)
+    tol = 2e-4 + 1e-2 * np.abs(want) + 1e-2 * spread
+    err = np.abs(want - got)
+    bad = np.argmax(err / tol)
+    assert (err <= tol).all(), f"element {bad}: {got[bad]} wanted {want[bad]} (err {err[bad]}, tol {tol[bad]})"
+    worst = float((err / tol).max())
+    assert worst < 0.5, f"worst error is {worst} of its tolerance"
+
+
+@pytest.mark.parametrize("heads,kv,hd,causal", [(4, 2, 128, True), (4, 4, 64, False), (4, 2, 64, False),
+                                               (4, 4, 128, True), (4, 4, 64, True), (4, 2, 64, True)])
+def test_fused_attention_cases(gpu, heads, kv, hd, causal):
+    # Odd on purpose: a query count that is not a whole tile, a cache with room to spare.
+    fused_attention_sized(gpu, heads, kv, hd, causal, 70, 33, 160, False)
+
+
+@pytest.mark.parametrize("args", [(8, 2, 128, True, 150, 0, 256, True), (8, 1, 128, True, 90, 17, 128, True),
+                                  (4, 4, 128, True, 200, 40, 256, True), (4, 2, 128, True, 130, 5, 138, True),
+                                  (4, 4, 64, False, 300, 0, 300, False)])
+def test_fused_attention_holds_at_the_prefill_shapes(gpu, args):
+    fused_attention_sized(gpu, *args)
+
+
+def test_an_uninstantiated_head_width_is_refused(gpu):
+    from ttsxabe_amd.gpu import UnsupportedAttention
+    assert not gpu.supports_flash(96, 4, 4)
+    z = torch.zeros(4 * 4 * 96, device="cuda")
+    with pytest.raises(UnsupportedAttention):
+        gpu.flash_attn(z, z, z, 4, 0, 4, 4, 96, 4, 1.0, False)
+    assert not gpu.supports_flash(128, 4, 3)
+
+
+def test_an_f16_cache_serves_the_same_attention_as_an_f32_one(gpu):
+    kv, hd, cap, n, group = 4, 128, 64, 37, 4
+    heads = kv * group
+    src = oracle.seq(n * kv * hd, 11)
+    k32 = torch.zeros(cap * kv * hd, device="cuda")
+    v32 = torch.zeros(cap * kv * hd, device="cuda")
+    k16 = torch.zeros(cap * kv * hd, dtype=torch.float16, device="cuda")
+    v16 = torch.zeros(cap * kv * hd, dtype=torch.float16, device="cuda")
+    dsrc = up(src)
+    for tr, d32, d16 in ((False, k32, k16), (True, v32, v16)):
+        gpu.cache_append(dsrc, 0, d32, n, kv, hd, cap, 0, tr)
+        gpu.cache_append_f16(dsrc, 0, d16, n, kv, hd, cap, 0, tr)
+    fq = up(oracle.seq(n * heads * hd, 13))
+    a = down(gpu.flash_attn(fq, k32, v32, n, 0, heads, kv, hd, cap, 0.1, True))
+    b = down(gpu.flash_attn_f16(fq, k16, v16, n, 0, heads, kv, hd, cap, 0.1, True))
+    scale = max(np.abs(a).max(), 1e-6)
+    assert np.abs(a - b).max() / scale < 2e-3
+
+
+@pytest.mark.parametrize("t,heads", [(150, 4), (1500, 20)])
+def test_the_encoder_attention_off_its_rows_is_the_split_path(gpu, t, heads):
+    hd = 64
+    d = heads * hd
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    qkv = oracle.seq(t * 3 * d, 611) * np.float32(3.0)
+    rows = qkv.reshape(t, 3 * d)
+    q = np.ascontiguousarray(rows[:, :d]) * np.float32(scale)  # the scaling pass, in f32
+    kcol = rows[:, d:2 * d].reshape(t, heads, hd)
+    vcol = rows[:, 2 * d:].reshape(t, heads, hd)
+    k = np.ascontiguousarray(kcol.transpose(1, 0, 2))          # split_heads   [h][t][hd]
+    v = np.ascontiguousarray(vcol.transpose(1, 2, 0))          # split_heads_t [h][hd][t]
+    ctx = gpu.flash_attn(up(q), up(k), up(v), t, 0, heads, heads, hd, t, 1.0, False)
+    want = down(ctx.to(torch.float16)).view(np.uint16)
+    got = down(gpu.flash_attn_rows(up(qkv), t, heads, hd, scale)).view(np.uint16)
+    bad = int((want != got).sum())
+    assert bad == 0, f"t {t} heads {heads}: {bad} of {want.size} differ"

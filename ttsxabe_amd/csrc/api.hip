@@ -1,0 +1,533 @@
+// The C ABI (include/llmtie_hip.h): argument checks in the reference's order
+// and with its error variants, then one launch. Mirrors the `impl Gpu`
+// attention methods of crates/llmtie-cuda/src/device.rs:5697-6410 and the
+// cache producers at :2849-3190, :5410-5470.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "../../include/llmtie_hip.h"
+#include "decode.h"
+#include "kvcache.h"
+#include "prefill.h"
+
+using namespace llmtie;
+
+namespace {
+
+thread_local llmtie_error g_err = {0, {0, 0, 0, 0}, {0}};
+
+int fail(int status, size_t f0, size_t f1, size_t f2, size_t f3, const char* fmt, ...) {
+    g_err.status = status;
+    g_err.field[0] = f0;
+    g_err.field[1] = f1;
+    g_err.field[2] = f2;
+    g_err.field[3] = f3;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err.message, sizeof g_err.message, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int ok() {
+    g_err.status = LLMTIE_OK;
+    g_err.message[0] = 0;
+    return LLMTIE_OK;
+}
+
+int unsupported(size_t hd, size_t heads, size_t kv) {
+    return fail(LLMTIE_UNSUPPORTED_ATTENTION, hd, heads, kv, 0,
+                "fused attention wants head_dim 64 or 128 and heads a multiple of kv_heads, got head_dim %zu, "
+                "%zu heads over %zu",
+                hd, heads, kv);
+}
+int overrun_slice(size_t at, size_t len) {
+    return fail(LLMTIE_SLICE_OVERRUN, at, len, 0, 0, "reading to %zu in a buffer of %zu", at, len);
+}
+int overrun_cache(size_t at, size_t cap) {
+    return fail(LLMTIE_CACHE_OVERRUN, at, cap, 0, 0, "appending at %zu to a cache with room for %zu", at, cap);
+}
+int odd_cap(size_t cap) {
+    return fail(LLMTIE_ODD_CACHE_CAPACITY, cap, 0, 0, 0, "an f16 cache with an odd capacity of %zu", cap);
+}
+int invalid(const char* what) { return fail(LLMTIE_INVALID_ARGUMENT, 0, 0, 0, 0, "%s is null", what); }
+int driver(const char* what, hipError_t e) {
+    if (e == hipErrorNoDevice || e == hipErrorInsufficientDriver)
+        return fail(LLMTIE_NO_DEVICE, 0, 0, 0, 0, "no usable HIP device: %s", hipGetErrorString(e));
+    return fail(LLMTIE_DRIVER, (size_t)e, 0, 0, 0, "%s: %s", what, hipGetErrorString(e));
+}
+int launched(const char* what, hipError_t e) { return e == hipSuccess ? ok() : driver(what, e); }
+
+hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Every kernel takes int extents; anything that does not fit is refused as
+// an overrun of the int range rather than silently wrapped.
+constexpr size_t IMAX = 0x7fffffff;
+
+}  // namespace
+
+struct llmtie_decode_scratch {
+    float* part = nullptr;
+    size_t part_cap = 0;  // floats
+    unsigned* ctr = nullptr;
+    size_t ctr_cap = 0;   // counters
+    int device = -1;
+};
+
+extern "C" {
+
+int llmtie_last_error(llmtie_error* out) {
+    if (out) *out = g_err;
+    return g_err.status;
+}
+
+const char* llmtie_version(void) { return "0.1.0"; }
+
+llmtie_decode_scratch* llmtie_decode_scratch_new(void) { return new llmtie_decode_scratch(); }
+
+void llmtie_decode_scratch_free(llmtie_decode_scratch* s) {
+    if (!s) return;
+    if (s->part) (void)hipFree(s->part);
+    if (s->ctr) (void)hipFree(s->ctr);
+    delete s;
+}
+
+int llmtie_supports_flash(size_t head_dim, size_t heads, size_t kv_heads) {
+    return (head_dim == 64 || head_dim == 128) && kv_heads > 0 && heads % kv_heads == 0 && heads > 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+// 16-query tiles per wave: the most that still leaves about two workgroups
+// per CU (256 CUs), so short prefills spread over the whole chip.
+int pick_nqt(size_t tq, size_t heads, int gb) {
+    if (const char* e = getenv("LLMTIE_PREFILL_NQT")) {
+        const int v = atoi(e);
+        if (v == 1 || v == 2 || v == 4) return v;
+    }
+    const int cands[3] = {4, 2, 1};
+    for (int nqt : cands) {
+        const size_t pb = 16 * nqt * (4 / gb);
+        const size_t wgs = ((tq + pb - 1) / pb) * (heads / gb);
+        if (wgs >= 512) return nqt;
+    }
+    return 1;
+}
+
+int prefill_common(void* stream, int kind, const float* q, size_t q_len, const void* k, size_t k_len, const void* v,
+                   size_t v_len, float* out, size_t out_len, size_t tq, size_t past, size_t heads, size_t kv_heads,
+                   size_t hd, size_t cap, float scale, int causal) {
+    if (!(hd == 64 || hd == 128) || kv_heads == 0 || heads % kv_heads != 0) return unsupported(hd, heads, kv_heads);
+    if (past + tq > cap) return overrun_cache(past + tq, cap);
+    if (heads * hd > IMAX || cap > IMAX || tq * heads * hd > (size_t)1 << 40) return overrun_slice(tq * heads * hd, IMAX);
+    if (q_len < tq * heads * hd) return overrun_slice(tq * heads * hd, q_len);
+    const size_t need = kv_heads * cap * hd;
+    if (k_len < need || v_len < need) return overrun_slice(need, std::min(k_len, v_len));
+    if (out_len < tq * heads * hd) return overrun_slice(tq * heads * hd, out_len);
+    if (tq == 0) return ok();
+    if (!q || !k || !v || !out) return invalid("a buffer");
+    const size_t group = heads / kv_heads;
+    const int gb = group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
+    PrefillArgs a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.tq = (int)tq;
+    a.past = (int)past;
+    a.heads = (int)heads;
+    a.kv_heads = (int)kv_heads;
+    a.cap = (int)cap;
+    a.scale = scale;
+    a.causal = causal ? 1 : 0;
+    a.gb = gb;
+    a.qs = (int)(heads * hd);
+    a.kvs = 0;
+    a.os = (int)(heads * hd);
+    a.scale_q = 0;
+    return launched("flash_attn", launch_prefill((int)hd, kind, pick_nqt(tq, heads, gb), a, S(stream)));
+}
+
+// Splits of one head: about `target` workgroups over the whole launch, each
+// wave taking whole 32-key blocks, and never more than the merge can hold.
+void plan_decode(size_t tk_max, size_t units, int& nit, int& splits) {
+    size_t target = 512;
+    if (const char* e = getenv("LLMTIE_DECODE_WGS")) target = std::max(1, atoi(e));
+    const size_t blocks = (tk_max + 31) / 32;
+    size_t want = std::max<size_t>(1, target / std::max<size_t>(1, units));
+    size_t per_wg = (blocks + want - 1) / want;           // 32-key blocks per workgroup
+    size_t n = std::max<size_t>(1, (per_wg + 3) / 4);     // per wave
+    if (const char* e = getenv("LLMTIE_DECODE_NIT")) n = std::max(1, atoi(e));
+    size_t span = 4 * n * 32;
+    while ((tk_max + span - 1) / span > (size_t)DECODE_MAX_SPLITS) {
+        ++n;
+        span = 4 * n * 32;
+    }
+    nit = (int)n;
+    splits = (int)((tk_max + span - 1) / span);
+}
+
+int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hipStream_t st) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return driver("hipGetDevice", e);
+    if (s->device != dev) {
+        // A scratch follows the device it is used on; switching starts over.
+        if (s->part) (void)hipFree(s->part);
+        if (s->ctr) (void)hipFree(s->ctr);
+        s->part = nullptr;
+        s->ctr = nullptr;
+        s->part_cap = s->ctr_cap = 0;
+        s->device = dev;
+    }
+    if (s->part_cap < part_floats) {
+        size_t want = 1024;
+        while (want < part_floats) want <<= 1;
+        if (s->part) (void)hipFree(s->part);
+        s->part = nullptr;
+        s->part_cap = 0;
+        e = hipMalloc(&s->part, want * sizeof(float));
+        if (e != hipSuccess) return driver("allocating", e);
+        s->part_cap = want;
+    }
+    if (s->ctr_cap < ctrs) {
+        size_t want = 64;
+        while (want < ctrs) want <<= 1;
+        if (s->ctr) (void)hipFree(s->ctr);
+        s->ctr = nullptr;
+        s->ctr_cap = 0;
+        e = hipMalloc(&s->ctr, want * sizeof(unsigned));
+        if (e != hipSuccess) return driver("allocating", e);
+        e = hipMemsetAsync(s->ctr, 0, want * sizeof(unsigned), st);
+        if (e != hipSuccess) return driver("zeroing", e);
+        s->ctr_cap = want;
+    }
+    return LLMTIE_OK;
+}
+
+// The checks and the launch behind every single-sequence decode
+// (device.rs:6224-6410).
+int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q_off, const void* k, size_t k_len,
+                  const void* v, size_t v_len, size_t heads, size_t kv_heads, size_t hd, size_t tk, size_t cap,
+                  float scale, int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len,
+                  size_t out_off, int8_t* twin, size_t twin_rows, size_t twin_k, bool has_twin) {
+    if (!(hd == 64 || hd == 128)) return unsupported(hd, heads, kv_heads);
+    if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 16) return unsupported(hd, heads, kv_heads);
+    if (tk == 0 || tk > cap) return overrun_cache(tk, cap);
+    const size_t esz = kind == KV_F32 ? 4 : 2;
+    if ((cap * esz) % 8 != 0) return odd_cap(cap);
+    if (cap > IMAX || kv_heads * cap * hd > ((size_t)1 << 40)) return overrun_slice(kv_heads * cap * hd, IMAX);
+    const size_t need = kv_heads * cap * hd;
+    if (k_len < need || v_len < need) return overrun_slice(need, std::min(k_len, v_len));
+    const size_t n = heads * hd;
+    if (q_len < q_off + n) return overrun_slice(q_off + n, q_len);
+    if (out_len < out_off + n) return overrun_slice(out_off + n, out_len);
+    if (out_off % 32 != 0) return fail(LLMTIE_RAGGED_BLOCK, out_off, 32, 0, 0, "a row of %zu in blocks of 32", out_off);
+    if (has_twin) {
+        if (twin_k != n || twin_rows * twin_k < out_off + n)
+            return fail(LLMTIE_MISMATCHED_Q8, twin_rows, twin_k, out_off / n + 1, n,
+                        "an int8 twin of %zu rows by %zu where %zu by %zu is needed", twin_rows, twin_k,
+                        out_off / n + 1, n);
+        if (!twin) return invalid("twin");
+    }
+    if (!q || !k || !v || !out) return invalid("a buffer");
+    if (!scratch) return invalid("scratch");
+    const size_t group = heads / kv_heads;
+    int nit, splits;
+    plan_decode(tk, kv_heads, nit, splits);
+    const size_t part = kv_heads * (size_t)splits * group * (hd + 2);
+    int r = ensure_scratch(scratch, part, kv_heads, S(stream));
+    if (r != LLMTIE_OK) return r;
+    DecodeArgs a;
+    memset(&a, 0, sizeof a);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    if (has_twin) {
+        a.twin_codes = twin;
+        a.twin_scales = reinterpret_cast<float*>(twin + twin_rows * twin_k);
+    }
+    a.part = scratch->part;
+    a.ctr = scratch->ctr;
+    a.q_off = (long)q_off;
+    a.out_off = (long)out_off;
+    a.tk = (int)tk;
+    a.cap = (int)cap;
+    a.kv_heads = (int)kv_heads;
+    a.group = (int)group;
+    a.score_l2 = (scale_q ? 1.0f : scale) * 1.4426950408889634f;
+    a.qscale = scale_q ? scale : 1.0f;
+    a.nit = nit;
+    a.splits = splits;
+    return launched("attn_decode", launch_decode((int)hd, kind, a, (int)kv_heads, 1, S(stream)));
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmtie_flash_attn(void* stream, const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                      size_t v_len, float* out, size_t out_len, size_t tq, size_t past, size_t heads,
+                      size_t kv_heads, size_t head_dim, size_t cap, float scale, int causal) {
+    return prefill_common(stream, PF_F32, q, q_len, k, k_len, v, v_len, out, out_len, tq, past, heads, kv_heads,
+                          head_dim, cap, scale, causal);
+}
+
+int llmtie_flash_attn_f16(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
+                          const uint16_t* v, size_t v_len, float* out, size_t out_len, size_t tq, size_t past,
+                          size_t heads, size_t kv_heads, size_t head_dim, size_t cap, float scale, int causal) {
+    if (!(head_dim == 64 || head_dim == 128)) return unsupported(head_dim, heads, kv_heads);
+    if (cap % 2 != 0) return odd_cap(cap);
+    return prefill_common(stream, PF_F16, q, q_len, k, k_len, v, v_len, out, out_len, tq, past, heads, kv_heads,
+                          head_dim, cap, scale, causal);
+}
+
+int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint16_t* out, size_t out_len, size_t t,
+                           size_t heads, size_t head_dim, float scale) {
+    if (head_dim != 64 || heads == 0) return unsupported(head_dim, heads, heads);
+    const size_t d = heads * head_dim;
+    if (d * 3 > IMAX || t > IMAX) return overrun_slice(t * 3 * d, IMAX);
+    if (qkv_len < t * 3 * d) return overrun_slice(t * 3 * d, qkv_len);
+    if (out_len < t * d) return overrun_slice(t * d, out_len);
+    if (t == 0) return ok();
+    if (!qkv || !out) return invalid("a buffer");
+    PrefillArgs a;
+    a.q = qkv;
+    a.k = qkv + d;
+    a.v = qkv + 2 * d;
+    a.out = out;
+    a.tq = (int)t;
+    a.past = 0;
+    a.heads = (int)heads;
+    a.kv_heads = (int)heads;
+    a.cap = (int)t;
+    a.scale = scale;
+    a.causal = 0;
+    a.gb = 1;
+    a.qs = (int)(3 * d);
+    a.kvs = (int)(3 * d);
+    a.os = (int)d;
+    a.scale_q = 1;
+    return launched("flash_attn_rows", launch_prefill(64, PF_ROWS, pick_nqt(t, heads, 1), a, S(stream)));
+}
+
+int llmtie_attn_decode_f16(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
+                           const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads, size_t head_dim,
+                           size_t tk, size_t cap, float scale, int scale_q, llmtie_decode_scratch* scratch,
+                           float* out, size_t out_len) {
+    return decode_common(stream, KV_F16, q, q_len, 0, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap, scale,
+                         scale_q, scratch, out, out_len, 0, nullptr, 0, 0, false);
+}
+
+int llmtie_attn_decode_f16_q(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
+                             const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads, size_t head_dim,
+                             size_t tk, size_t cap, float scale, int scale_q, llmtie_decode_scratch* scratch,
+                             float* out, size_t out_len, int8_t* twin, size_t twin_len) {
+    const size_t n = heads * head_dim;
+    if (twin_len < n + (n / 32) * 4) return overrun_slice(n + (n / 32) * 4, twin_len);
+    if (n % 32 != 0) return fail(LLMTIE_RAGGED_BLOCK, n, 32, 0, 0, "a row of %zu in blocks of 32", n);
+    return decode_common(stream, KV_F16, q, q_len, 0, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap, scale,
+                         scale_q, scratch, out, out_len, 0, twin, 1, n, true);
+}
+
+int llmtie_attn_decode_f16_q_row(void* stream, const float* q, size_t q_len, size_t q_off, const uint16_t* k,
+                                 size_t k_len, const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads,
+                                 size_t head_dim, size_t tk, size_t cap, float scale, int scale_q,
+                                 llmtie_decode_scratch* scratch, float* out, size_t out_len, int8_t* twin,
+                                 size_t twin_rows, size_t twin_k, size_t row) {
+    return decode_common(stream, KV_F16, q, q_len, q_off, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap,
+                         scale, scale_q, scratch, out, out_len, row * heads * head_dim, twin, twin_rows, twin_k,
+                         true);
+}
+
+int llmtie_attn_decode(void* stream, const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                       size_t v_len, size_t heads, size_t kv_heads, size_t head_dim, size_t tk, size_t cap,
+                       float scale, int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len) {
+    return decode_common(stream, KV_F32, q, q_len, 0, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap, scale,
+                         scale_q, scratch, out, out_len, 0, nullptr, 0, 0, false);
+}
+
+int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, const int8_t* k_codes,
+                                const uint16_t* k_scales, const int8_t* v_codes, const uint16_t* v_scales,
+                                size_t slots, const int32_t* tk_dev, const int32_t* slot_dev, size_t nseq,
+                                size_t max_tk, size_t heads, size_t kv_heads, size_t head_dim, size_t cap,
+                                float scale, int scale_q, llmtie_decode_scratch* scratch, float* out,
+                                size_t out_len) {
+    if (!(head_dim == 64 || head_dim == 128)) return unsupported(head_dim, heads, kv_heads);
+    if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 16) return unsupported(head_dim, heads, kv_heads);
+    if (cap % 32 != 0) return fail(LLMTIE_RAGGED_BLOCK, cap, 32, 0, 0, "a Q8_0 cache capacity of %zu in blocks of 32", cap);
+    if (max_tk == 0 || max_tk > cap) return overrun_cache(max_tk, cap);
+    if (cap > IMAX || nseq > 65535 || slots > IMAX) return overrun_slice(nseq, 65535);
+    const size_t n = heads * head_dim;
+    if (q_len < nseq * n) return overrun_slice(nseq * n, q_len);
+    if (out_len < nseq * n) return overrun_slice(nseq * n, out_len);
+    if (nseq == 0) return ok();
+    if (!q || !k_codes || !k_scales || !v_codes || !v_scales || !tk_dev || !slot_dev || !out) return invalid("a buffer");
+    if (!scratch) return invalid("scratch");
+    const size_t group = heads / kv_heads;
+    int nit, splits;
+    plan_decode(max_tk, kv_heads * nseq, nit, splits);
+    const size_t part = nseq * kv_heads * (size_t)splits * group * (head_dim + 2);
+    int r = ensure_scratch(scratch, part, nseq * kv_heads, S(stream));
+    if (r != LLMTIE_OK) return r;
+    DecodeArgs a;
+    memset(&a, 0, sizeof a);
+    a.q = q;
+    a.k = k_codes;
+    a.v = v_codes;
+    a.ks = k_scales;
+    a.vs = v_scales;
+    a.out = out;
+    a.part = scratch->part;
+    a.ctr = scratch->ctr;
+    a.tk_arr = tk_dev;
+    a.slot_arr = slot_dev;
+    a.q_stride = (long)n;
+    a.out_stride = (long)n;
+    a.tk = (int)max_tk;
+    a.slots = (int)slots;
+    a.cap = (int)cap;
+    a.kv_heads = (int)kv_heads;
+    a.group = (int)group;
+    a.score_l2 = (scale_q ? 1.0f : scale) * 1.4426950408889634f;
+    a.qscale = scale_q ? scale : 1.0f;
+    a.nit = nit;
+    a.splits = splits;
+    return launched("attn_decode_q8_batch", launch_decode((int)head_dim, KV_Q8, a, (int)kv_heads, (int)nseq, S(stream)));
+}
+
+int llmtie_rope(void* stream, float* x, size_t x_len, size_t off, const float* freq_div, size_t t, size_t heads,
+                size_t head_dim, float theta, size_t first) {
+    if (off + t * heads * head_dim > x_len) return overrun_slice(off + t * heads * head_dim, x_len);
+    if (head_dim % 2 != 0) return fail(LLMTIE_ODD_HEAD_DIM, head_dim, 0, 0, 0, "a rotary head of odd width %zu", head_dim);
+    if (t * heads * head_dim == 0) return ok();
+    if (!x) return invalid("x");
+    return launched("rope", launch_rope(x, (long)off, freq_div, (int)t, (int)heads, (int)head_dim, theta, (int)first,
+                                        S(stream)));
+}
+
+static int append_common(void* stream, const float* src, size_t src_len, size_t src_off, void* dst, size_t dst_len,
+                         int f16, size_t n, size_t kv, size_t hd, size_t cap, size_t past, int tr) {
+    if (past + n > cap) return overrun_cache(past + n, cap);
+    if (f16 && cap % 2 != 0) return odd_cap(cap);
+    const size_t total = n * kv * hd;
+    if (src_off + total > src_len) return overrun_slice(src_off + total, src_len);
+    if (kv * cap * hd > dst_len) return overrun_slice(kv * cap * hd, dst_len);
+    if (total == 0) return ok();
+    if (!src || !dst) return invalid("a buffer");
+    return launched("cache_append", launch_append(src, (long)src_off, dst, f16, tr, (int)n, (int)kv, (int)hd,
+                                                  (int)cap, (int)past, S(stream)));
+}
+
+int llmtie_cache_append(void* stream, const float* src, size_t src_len, size_t src_off, float* dst, size_t dst_len,
+                        size_t n, size_t kv_heads, size_t head_dim, size_t cap, size_t past, int transposed) {
+    return append_common(stream, src, src_len, src_off, dst, dst_len, 0, n, kv_heads, head_dim, cap, past, transposed);
+}
+
+int llmtie_cache_append_f16(void* stream, const float* src, size_t src_len, size_t src_off, uint16_t* dst,
+                            size_t dst_len, size_t n, size_t kv_heads, size_t head_dim, size_t cap, size_t past,
+                            int transposed) {
+    return append_common(stream, src, src_len, src_off, dst, dst_len, 1, n, kv_heads, head_dim, cap, past, transposed);
+}
+
+int llmtie_rope_cache_f16(void* stream, float* q, size_t q_len, size_t q_off, const float* k, size_t k_len,
+                          size_t k_off, const float* v, size_t v_len, size_t v_off, const float* freq_div,
+                          size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, uint16_t* kc,
+                          uint16_t* vc, size_t cache_len, size_t cap) {
+    if (pos >= cap) return overrun_cache(pos + 1, cap);
+    if (cap % 2 != 0) return odd_cap(cap);
+    if (head_dim % 2 != 0) return fail(LLMTIE_ODD_HEAD_DIM, head_dim, 0, 0, 0, "a rotary head of odd width %zu", head_dim);
+    if (q_off + heads * head_dim > q_len) return overrun_slice(q_off + heads * head_dim, q_len);
+    if (k_off + kv_heads * head_dim > k_len) return overrun_slice(k_off + kv_heads * head_dim, k_len);
+    if (v_off + kv_heads * head_dim > v_len) return overrun_slice(v_off + kv_heads * head_dim, v_len);
+    if (cache_len < cap * kv_heads * head_dim) return overrun_slice(cap * kv_heads * head_dim, cache_len);
+    if (!q || !k || !v || !kc || !vc) return invalid("a buffer");
+    return launched("rope_cache_f16",
+                    launch_rope_cache_f16(q, (long)q_off, k, (long)k_off, v, (long)v_off, freq_div, (int)heads,
+                                          (int)kv_heads, (int)head_dim, theta, (int)pos, kc, vc, (int)cap, S(stream)));
+}
+
+static int grow_common(void* stream, const void* src, size_t src_len, void* dst, size_t dst_len, int esz, size_t kv,
+                       size_t hd, size_t cap, size_t new_cap, size_t live, int tr) {
+    if (live > cap || new_cap < cap) return overrun_cache(std::max(live, cap), std::min(new_cap, cap));
+    size_t rows, len, ss, ds;
+    if (!tr) {
+        rows = kv;
+        len = live * hd;
+        ss = cap * hd;
+        ds = new_cap * hd;
+    } else {
+        rows = kv * hd;
+        len = live;
+        ss = cap;
+        ds = new_cap;
+    }
+    if (rows * ss > src_len) return overrun_slice(rows * ss, src_len);
+    if (rows * ds > dst_len) return overrun_slice(rows * ds, dst_len);
+    if (rows * len == 0) return ok();
+    if (!src || !dst) return invalid("a buffer");
+    return launched("cache_grow", launch_grow(src, dst, esz, (int)rows, (int)len, (int)ss, (int)ds, S(stream)));
+}
+
+int llmtie_cache_grow(void* stream, const float* src, size_t src_len, float* dst, size_t dst_len, size_t kv_heads,
+                      size_t head_dim, size_t cap, size_t new_cap, size_t live, int transposed) {
+    return grow_common(stream, src, src_len, dst, dst_len, 4, kv_heads, head_dim, cap, new_cap, live, transposed);
+}
+
+int llmtie_cache_grow_f16(void* stream, const uint16_t* src, size_t src_len, uint16_t* dst, size_t dst_len,
+                          size_t kv_heads, size_t head_dim, size_t cap, size_t new_cap, size_t live,
+                          int transposed) {
+    return grow_common(stream, src, src_len, dst, dst_len, 2, kv_heads, head_dim, cap, new_cap, live, transposed);
+}
+
+static int q8_cache_checks(size_t hd, size_t heads, size_t kv, size_t cap, size_t slots, size_t slot) {
+    if (!(hd == 64 || hd == 128)) return unsupported(hd, heads, kv);
+    if (cap % 32 != 0) return fail(LLMTIE_RAGGED_BLOCK, cap, 32, 0, 0, "a Q8_0 cache capacity of %zu in blocks of 32", cap);
+    if (slot >= slots) return overrun_slice(slot + 1, slots);
+    return LLMTIE_OK;
+}
+
+int llmtie_kv_q8_append(void* stream, const float* k, size_t k_len, size_t k_off, const float* v, size_t v_len,
+                        size_t v_off, int8_t* k_codes, uint16_t* k_scales, int8_t* v_codes, uint16_t* v_scales,
+                        size_t slots, size_t slot, size_t n, size_t kv_heads, size_t head_dim, size_t cap,
+                        size_t past) {
+    int r = q8_cache_checks(head_dim, kv_heads, kv_heads, cap, slots, slot);
+    if (r != LLMTIE_OK) return r;
+    if (past + n > cap) return overrun_cache(past + n, cap);
+    const size_t total = n * kv_heads * head_dim;
+    if (k_off + total > k_len) return overrun_slice(k_off + total, k_len);
+    if (v_off + total > v_len) return overrun_slice(v_off + total, v_len);
+    if (total == 0) return ok();
+    if (!k || !v || !k_codes || !k_scales || !v_codes || !v_scales) return invalid("a buffer");
+    return launched("kv_q8_append", launch_append_q8(k, (long)k_off, v, (long)v_off, k_codes, k_scales, v_codes,
+                                                     v_scales, (int)slot, (int)n, (int)kv_heads, (int)head_dim,
+                                                     (int)cap, (int)past, S(stream)));
+}
+
+int llmtie_rope_cache_q8(void* stream, float* q, size_t q_len, size_t q_off, const float* k, size_t k_len,
+                         size_t k_off, const float* v, size_t v_len, size_t v_off, const float* freq_div,
+                         size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, int8_t* k_codes,
+                         uint16_t* k_scales, int8_t* v_codes, uint16_t* v_scales, size_t slots, size_t slot,
+                         size_t cap) {
+    int r = q8_cache_checks(head_dim, heads, kv_heads, cap, slots, slot);
+    if (r != LLMTIE_OK) return r;
+    if (pos >= cap) return overrun_cache(pos + 1, cap);
+    if (q_off + heads * head_dim > q_len) return overrun_slice(q_off + heads * head_dim, q_len);
+    if (k_off + kv_heads * head_dim > k_len) return overrun_slice(k_off + kv_heads * head_dim, k_len);
+    if (v_off + kv_heads * head_dim > v_len) return overrun_slice(v_off + kv_heads * head_dim, v_len);
+    if (!q || !k || !v || !k_codes || !k_scales || !v_codes || !v_scales) return invalid("a buffer");
+    return launched("rope_cache_q8", launch_rope_cache_q8(q, (long)q_off, k, (long)k_off, v, (long)v_off, freq_div,
+                                                          (int)heads, (int)kv_heads, (int)head_dim, theta, (int)pos,
+                                                          k_codes, k_scales, v_codes, v_scales, (int)slot, (int)cap,
+                                                          S(stream)));
+}
+
+}  // extern "C"

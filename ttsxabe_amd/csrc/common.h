@@ -1,0 +1,103 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// Everything here is written for CDNA4 directly: 64-lane wavefronts, the
+// v_mfma_f32_16x16x32_f16 matrix instruction, v_exp_f32 for exponentials and
+// v_cvt_f16_f32 (round to nearest even) for every f32 -> f16 step.
+//
+// MFMA 16x16x32 f16 operand layout, as used by every kernel in this library
+// (lane l of a 64-lane wave; `col = l & 15`, `grp = l >> 4`):
+//   A (16 x 32):  lane l holds A[row = col][k = kslot(grp, j)], j = 0..7
+//   B (32 x 16):  lane l holds B[k = kslot(grp, j)][col = col], j = 0..7
+//   D (16 x 16):  lane l holds D[row = 4 * grp + r][col = col],  r = 0..3
+// A and B name the same contraction slot for the same (grp, j), whatever the
+// hardware's internal order of k is, so a kernel is free to decide which
+// element of its own problem sits in slot (grp, j) as long as it decides it
+// the same way for both operands. The kernels use that freedom to land the
+// softmax probabilities straight in B-operand order without an LDS round trip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+#define LLMTIE_WAVE 64
+#define LLMTIE_LOG2E 1.4426950408889634f
+
+__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 2^x on the transcendental unit; 2^-inf is exactly 0.
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float ninf() { return __builtin_bit_cast(float, 0xff800000u); }
+
+// f32 -> f16, IEEE round to nearest even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ half_t to_h(float x) { return (half_t)x; }
+
+// x = hi + lo with hi = f16(x), lo = f16(x - hi): the pair carries ~22 bits
+// of x, so an MFMA against both halves reproduces an f32 product to about
+// 2^-22 relative instead of f16's 2^-11.
+__device__ __forceinline__ void split_h(float x, half_t& hi, half_t& lo) {
+    hi = (half_t)x;
+    lo = (half_t)(x - (float)hi);
+}
+
+__device__ __forceinline__ half8 zero_h8() {
+    half8 z;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) z[j] = (half_t)0.0f;
+    return z;
+}
+
+__device__ __forceinline__ floatx4 zero_f4() {
+    floatx4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    return z;
+}
+
+// 16 bytes as eight halves; `p` must be 16-byte aligned.
+__device__ __forceinline__ half8 ld_h8(const void* p) {
+    return *reinterpret_cast<const half8*>(p);
+}
+
+// Eight halves from an address that is only 4-byte aligned.
+__device__ __forceinline__ half8 ld_h8_a4(const uint16_t* p) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
+    uint32_t x0 = w[0], x1 = w[1], x2 = w[2], x3 = w[3];
+    half8 r;
+    uint32_t ws[4] = {x0, x1, x2, x3};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[2 * i] = __builtin_bit_cast(half_t, (uint16_t)(ws[i] & 0xffffu));
+        r[2 * i + 1] = __builtin_bit_cast(half_t, (uint16_t)(ws[i] >> 16));
+    }
+    return r;
+}
+
+// Eight int8 codes (8 bytes, 8-byte aligned) as eight exact halves.
+__device__ __forceinline__ half8 ld_q8x8(const int8_t* p) {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[i] = (half_t)(float)(int8_t)((w.x >> (8 * i)) & 0xff);
+        r[4 + i] = (half_t)(float)(int8_t)((w.y >> (8 * i)) & 0xff);
+    }
+    return r;
+}
+
+// Cross-lane reductions over the four lanes that share `col` (xor 16, 32).
+__device__ __forceinline__ float max4grp(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+__device__ __forceinline__ float sum4grp(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}

@@ -1,0 +1,42 @@
+// Launch interface of the decode attention kernel (decode.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmtie {
+
+enum KvKind { KV_F16 = 0, KV_F32 = 1, KV_Q8 = 2 };
+
+// Upper bound on splits per head: the merging workgroup keeps one weight per
+// split and query head in LDS.
+constexpr int DECODE_MAX_SPLITS = 256;
+
+struct DecodeArgs {
+    const float* q;          // query rows, f32
+    const void* k;           // K values or codes
+    const void* v;           // V^T values or codes
+    const uint16_t* ks;      // Q8_0 scales of K (f16 bits), else null
+    const uint16_t* vs;      // Q8_0 scales of V (f16 bits), else null
+    float* out;              // context rows, f32
+    int8_t* twin_codes;      // int8 twin of the context, or null
+    float* twin_scales;      // its per-32 scales
+    float* part;             // split partials
+    unsigned* ctr;           // one arrival counter per (sequence, kv head), zero between calls
+    const int* tk_arr;       // per-sequence live lengths (batched) or null
+    const int* slot_arr;     // per-sequence cache slot (batched) or null
+    long q_off, q_stride;    // element offset of sequence 0's query; elements per sequence
+    long out_off, out_stride;
+    int tk;                  // live length, or the bound every tk_arr entry is clamped to
+    int slots;               // cache slots (batched)
+    int cap;                 // positions per cache row
+    int kv_heads;            // kv heads per slot
+    int group;               // query heads per kv head (<= 16)
+    float score_l2;          // raw dot product -> log2-unit score
+    float qscale;            // applied to q before it is split
+    int nit;                 // 32-key blocks per wave per split
+    int splits;              // grid.x: splits of the longest sequence
+};
+
+hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);
+
+}  // namespace llmtie

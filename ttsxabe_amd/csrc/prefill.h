@@ -1,0 +1,33 @@
+// Launch interface of the prefill (flash) attention kernel (prefill.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmtie {
+
+// Where K and V come from.
+enum PfKind {
+    PF_F16 = 0,   // f16 caches: K [kv][cap][hd], V [kv][hd][cap]
+    PF_F32 = 1,   // the same layout at f32
+    PF_ROWS = 2,  // columns of a stacked [t, 3d] f32 q/k/v product (Whisper encoder)
+};
+
+struct PrefillArgs {
+    const float* q;   // [tq, qs] f32; head h at column h*hd
+    const void* k;    // cache base, or the K column block of the stacked rows
+    const void* v;    // cache base, or the V column block of the stacked rows
+    void* out;        // [tq, os] f32, or f16 for PF_ROWS
+    int tq, past, heads, kv_heads, cap;
+    float scale;
+    int causal;
+    int gb;           // query heads per workgroup (1, 2 or 4)
+    int qs;           // q row stride, elements
+    int kvs;          // PF_ROWS: k/v row stride, elements
+    int os;           // out row stride, elements
+    int scale_q;      // the scale goes on q before rounding (else on the scores)
+};
+
+// nqt: 16-query tiles per wave (1, 2 or 4).
+hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st);
+
+}  // namespace llmtie

@@ -1,0 +1,321 @@
+// Flash-style prefill attention for gfx950 (causal GQA, non-causal encoder).
+//
+// Replaces the reference's `flash_attn_impl` and its entries `flash_attn`,
+// `flash_attn_h`, `flash_attn_64`, `flash_attn_64_rows`
+// (crates/llmtie-cuda/src/kernels.rs:3026-3311).
+//
+// Arithmetic (the reference's, kernels.rs:2955-2961): q (times the scale when
+// `scale_q`) rounded to f16, K and V rounded to f16, S = Q K^T accumulated at
+// f32 on MFMA, the running max in log2 units with scale * log2(e) folded in,
+// probabilities rounded to f16 on their way into P V, the normaliser summed at
+// f32 from the unrounded probabilities, and O / l at the end.
+//
+// Work decomposition. A workgroup is four waves. Like the reference, the
+// waves of a workgroup are the `gb` query heads of one GQA group (so one K/V
+// tile in LDS serves all of them) times 4/gb position blocks. A wave owns
+// 16 * NQT query positions of one head; Q lives in registers as MFMA B
+// operands for the whole kernel.
+//
+// Per 64-key tile (staged global -> registers -> LDS, the next tile's loads in
+// flight while this one is computed) a wave computes S^T = K Q^T with
+// v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims read from LDS, B = 32 dims x
+// 16 queries from registers, each A fragment reused across the NQT query
+// tiles. A-row m of tile (half, T) is key 32*half + 8*(m/4) + 4T + m%4, which
+// leaves lane l holding the scores of keys 32*half + 8*grp + 0..7 for its
+// query: the B-operand slots of O^T = V^T P^T over that half's 32 keys. P is
+// therefore rounded to f16 in registers and never written to LDS; the V^T
+// A-operand is one 16-byte row segment of the [d][key] tile.
+//
+// LDS rows are XOR-swizzled by 16-byte chunk so that the eight rows one
+// ds_read_b128 phase touches land on distinct banks.
+#include "common.h"
+#include "prefill.h"
+
+namespace llmtie {
+
+constexpr int PW = 4;    // waves per workgroup
+constexpr int PT = PW * LLMTIE_WAVE;
+constexpr int KT = 64;   // keys per LDS tile
+
+// Physical 16-byte chunk of logical chunk c in K-tile row r.
+template <int HD>
+__device__ __forceinline__ int swz_k(int r, int c) {
+    int x = (r & 3) | (((r >> 3) & 1) << 2);
+    if constexpr (HD / 8 >= 16) x |= ((r >> 4) & 1) << 3;
+    return c ^ x;
+}
+// Physical chunk of logical chunk c (8 keys) in V^T-tile row d.
+__device__ __forceinline__ int swz_v(int d, int c) { return c ^ (d & 7); }
+
+template <int HD, int KIND>
+struct Stage {
+    // Per thread: K chunks and V chunks of one tile, already f16.
+    static constexpr int KC = KT * (HD / 8) / PT;  // K chunks per thread
+    static constexpr int VC = HD * (KT / 8) / PT;  // V chunks per thread
+    half8 k[KC];
+    half8 v[VC];
+};
+
+template <int HD, int KIND>
+__device__ __forceinline__ half8 fetch8(const void* base, size_t off, int n, bool al) {
+    // Eight consecutive elements at `off`, zero past `n` valid ones.
+    half8 r = zero_h8();
+    if (n <= 0) return r;
+    if constexpr (KIND == PF_F16) {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(base) + off;
+        if (n >= 8 && al) return ld_h8(p);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (j < n) r[j] = __builtin_bit_cast(half_t, p[j]);
+        return r;
+    } else {
+        const float* p = reinterpret_cast<const float*>(base) + off;
+        if (n >= 8 && al) {
+            const float4 a = reinterpret_cast<const float4*>(p)[0];
+            const float4 b = reinterpret_cast<const float4*>(p)[1];
+            r[0] = to_h(a.x); r[1] = to_h(a.y); r[2] = to_h(a.z); r[3] = to_h(a.w);
+            r[4] = to_h(b.x); r[5] = to_h(b.y); r[6] = to_h(b.z); r[7] = to_h(b.w);
+            return r;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (j < n) r[j] = to_h(p[j]);
+        return r;
+    }
+}
+
+template <int HD, int KIND, int NQT>
+__global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
+    constexpr int NS = HD / 32;   // contraction steps of S
+    constexpr int NT = HD / 16;   // d tiles of O^T
+    constexpr int QPW = 16 * NQT;
+    constexpr int KCH = HD / 8;   // 16-byte chunks per K row
+    using St = Stage<HD, KIND>;
+
+    __shared__ __attribute__((aligned(16))) half_t ks[KT * HD];
+    __shared__ __attribute__((aligned(16))) half_t vs[HD * KT];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int gb = a.gb;
+    const int pb = QPW * (PW / gb);
+    const int group = a.heads / a.kv_heads;
+    // Heaviest (latest) position blocks first under a causal mask.
+    const int bx = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int h = blockIdx.y * gb + wave % gb;
+    const int kh = (blockIdx.y * gb) / group;
+    const int bp0 = bx * pb;
+    const int p0 = bp0 + (wave / gb) * QPW;
+    const int ktot = a.past + a.tq;
+    const int kend = a.causal ? min(ktot, a.past + bp0 + pb) : ktot;
+    const int wlim = a.causal ? min(a.past + p0 + QPW - 1, ktot - 1) : ktot - 1;
+
+    // Source addressing. Off a cache, K row p of head kh is at (kh*cap + p)*HD
+    // and V^T row d at (kh*HD + d)*cap. Off rows, both are p*kvs + kh*HD.
+    const bool rows = KIND == PF_ROWS;
+    const size_t kbase = rows ? (size_t)kh * HD : (size_t)kh * a.cap * HD;
+    const size_t vbase = rows ? (size_t)kh * HD : (size_t)kh * HD * a.cap;
+    const size_t krs = rows ? (size_t)a.kvs : (size_t)HD;
+    const bool kal = rows ? (a.kvs % 4 == 0) : true;
+    const bool val = rows ? kal : (KIND == PF_F16 ? a.cap % 8 == 0 : a.cap % 4 == 0);
+    constexpr int SK = KIND == PF_ROWS ? PF_F32 : KIND;
+
+    auto load_tile = [&](int kv0, St& st) {
+#pragma unroll
+        for (int i = 0; i < St::KC; ++i) {
+            const int id = tid + PT * i;
+            const int r = id / KCH, c = id % KCH;
+            st.k[i] = fetch8<HD, SK>(a.k, kbase + (size_t)(kv0 + r) * krs + 8 * c, kv0 + r < kend ? 8 : 0, kal);
+        }
+#pragma unroll
+        for (int i = 0; i < St::VC; ++i) {
+            const int id = tid + PT * i;
+            if constexpr (KIND == PF_ROWS) {
+                // V rows [key][d]: chunk = 8 dims of one key.
+                const int r = id / KCH, c = id % KCH;
+                st.v[i] = fetch8<HD, SK>(a.v, vbase + (size_t)(kv0 + r) * krs + 8 * c, kv0 + r < kend ? 8 : 0, val);
+            } else {
+                const int d = id / (KT / 8), c = id % (KT / 8);
+                const int p = kv0 + 8 * c;
+                st.v[i] = fetch8<HD, SK>(a.v, vbase + (size_t)d * a.cap + p, min(8, kend - p), val);
+            }
+        }
+    };
+    auto store_tile = [&](const St& st) {
+#pragma unroll
+        for (int i = 0; i < St::KC; ++i) {
+            const int id = tid + PT * i;
+            const int r = id / KCH, c = id % KCH;
+            *reinterpret_cast<half8*>(&ks[r * HD + 8 * swz_k<HD>(r, c)]) = st.k[i];
+        }
+#pragma unroll
+        for (int i = 0; i < St::VC; ++i) {
+            const int id = tid + PT * i;
+            if constexpr (KIND == PF_ROWS) {
+                const int key = id / KCH, c = id % KCH;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int d = 8 * c + j;
+                    vs[d * KT + 8 * swz_v(d, key >> 3) + (key & 7)] = st.v[i][j];
+                }
+            } else {
+                const int d = id / (KT / 8), c = id % (KT / 8);
+                *reinterpret_cast<half8*>(&vs[d * KT + 8 * swz_v(d, c)]) = st.v[i];
+            }
+        }
+    };
+
+    // Q as B operands: qb[u][s] holds dims 32s + 8grp + 0..7 of query p0 + 16u + col.
+    const float qsc = a.scale_q ? a.scale : 1.0f;
+    half8 qb[NQT][NS];
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        const int r = p0 + 16 * u + col;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            half8 x = zero_h8();
+            if (r < a.tq) {
+                const float4* p = reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 32 * s + 8 * grp);
+                const float4 x0 = p[0], x1 = p[1];
+                x[0] = to_h(x0.x * qsc); x[1] = to_h(x0.y * qsc); x[2] = to_h(x0.z * qsc); x[3] = to_h(x0.w * qsc);
+                x[4] = to_h(x1.x * qsc); x[5] = to_h(x1.y * qsc); x[6] = to_h(x1.z * qsc); x[7] = to_h(x1.w * qsc);
+            }
+            qb[u][s] = x;
+        }
+    }
+
+    floatx4 o[NT][NQT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) o[t][u] = zero_f4();
+    float m[NQT], l[NQT], lim[NQT];
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        m[u] = ninf();
+        l[u] = 0.0f;
+        const int r = p0 + 16 * u + col;
+        lim[u] = (float)(a.causal ? min(a.past + r, ktot - 1) : ktot - 1);
+    }
+    const float sl2 = (a.scale_q ? 1.0f : a.scale) * LLMTIE_LOG2E;
+
+    St st;
+    if (kend > 0) load_tile(0, st);
+    for (int kv0 = 0; kv0 < kend; kv0 += KT) {
+        __syncthreads();  // previous tile fully consumed
+        store_tile(st);
+        __syncthreads();
+        if (kv0 + KT < kend) load_tile(kv0 + KT, st);
+        if (kv0 > wlim) continue;
+
+        // S^T for the 64 keys: sc[hf][T][u], lane holds keys 32hf + 8grp + 4T + r.
+        floatx4 sc[2][2][NQT];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+#pragma unroll
+                for (int u = 0; u < NQT; ++u) sc[hf][T][u] = zero_f4();
+                const int r = 32 * hf + 8 * (col >> 2) + 4 * T + (col & 3);
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const half8 af = *reinterpret_cast<const half8*>(&ks[r * HD + 8 * swz_k<HD>(r, 4 * s + grp)]);
+#pragma unroll
+                    for (int u = 0; u < NQT; ++u) sc[hf][T][u] = mfma16(af, qb[u][s], sc[hf][T][u]);
+                }
+            }
+
+        // Online softmax per query tile.
+        half8 pb[2][NQT];
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) {
+            float mx = ninf();
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int key = kv0 + 32 * hf + 8 * grp + 4 * T + r;
+                        const float s = (float)key <= lim[u] ? sc[hf][T][u][r] * sl2 : ninf();
+                        sc[hf][T][u][r] = s;
+                        mx = fmaxf(mx, s);
+                    }
+            mx = max4grp(mx);
+            const float mn = fmaxf(m[u], mx);
+            // A row whose every key so far is masked keeps m = -inf; its
+            // factor and probabilities are then 0, never NaN.
+            const float fac = mn == ninf() ? 1.0f : ex2(m[u] - mn);
+            const float msub = mn == ninf() ? 0.0f : mn;
+            m[u] = mn;
+            float ps = 0.0f;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                half8 p;
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = ex2(sc[hf][T][u][r] - msub);
+                        ps += e;
+                        p[4 * T + r] = to_h(e);
+                    }
+                pb[hf][u] = p;
+            }
+            l[u] = l[u] * fac + ps;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[t][u] *= fac;
+        }
+
+        // O^T += V^T P^T.
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int d = 16 * t + col;
+                const half8 af = *reinterpret_cast<const half8*>(&vs[d * KT + 8 * swz_v(d, 4 * hf + grp)]);
+#pragma unroll
+                for (int u = 0; u < NQT; ++u) o[t][u] = mfma16(af, pb[hf][u], o[t][u]);
+            }
+    }
+
+    // O / l, stored: lane writes dims 16t + 4grp + 0..3 of query p0 + 16u + col.
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        const float lt = sum4grp(l[u]);
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const int r = p0 + 16 * u + col;
+        if (r >= a.tq) continue;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const size_t off = (size_t)r * a.os + (size_t)h * HD + 16 * t + 4 * grp;
+            if constexpr (KIND == PF_ROWS) {
+                half4 y;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[i] = to_h(o[t][u][i] * inv);
+                *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(a.out) + off) = y;
+            } else {
+                float4 y = make_float4(o[t][u][0] * inv, o[t][u][1] * inv, o[t][u][2] * inv, o[t][u][3] * inv);
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + off) = y;
+            }
+        }
+    }
+}
+
+hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st) {
+    const int pb = 16 * nqt * (PW / a.gb);
+    dim3 grid((a.tq + pb - 1) / pb, a.heads / a.gb), block(PT);
+#define L(HD, KIND, NQ)                                                                      \
+    if (hd == HD && kind == KIND && nqt == NQ) {                                             \
+        hipLaunchKernelGGL((flash_prefill_kernel<HD, KIND, NQ>), grid, block, 0, st, a);     \
+        return hipGetLastError();                                                            \
+    }
+#define LK(HD, KIND) L(HD, KIND, 1) L(HD, KIND, 2) L(HD, KIND, 4)
+    LK(64, PF_F16) LK(128, PF_F16) LK(64, PF_F32) LK(128, PF_F32) LK(64, PF_ROWS)
+#undef LK
+#undef L
+    return hipErrorInvalidValue;
+}
+
+}  // namespace llmtie
