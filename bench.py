@@ -1,0 +1,309 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused-attention hot path on one MI355X.
+
+Headline (BASELINE.json `metric`, configs[1]): Llama-3-8B GQA decode
+(32 query / 8 KV heads, head_dim 128, 4096-position f16 cache, batch 1). A
+step is one decoded token through a 32-layer stack: 32 decode-attention
+launches, each over its own layer's KV cache, so the 537 MB touched per step
+is more than twice the 256 MB Infinity Cache and the bytes come from HBM. The
+step is captured once in a HIP graph and replayed (no host work in the timed
+region). `value` = algorithmic bytes (2 * kv * tk * hd * 2 per layer, the
+reference's bench_attn.rs:167 formula) / step time.
+
+Secondary lines (prefill TFLOP/s, Whisper, batched Q8_0 decode) are measured
+the same way and reported under `secondary`. The CPU baseline is the oracle's
+C restatement of the reference's scalar decode chain, timed on this host.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+F16_PEAK_TFLOPS = 2500.0     # MI355X dense f16 MFMA, TFLOP/s
+LLC_BYTES = 256 * 2 ** 20    # Infinity Cache
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def rotate_layers(bytes_per_layer: int, want: int) -> int:
+    """Layers so that one step touches at least 2x the last-level cache."""
+    return max(want, math.ceil(2 * LLC_BYTES / max(1, bytes_per_layer)))
+
+
+class Timer:
+    """Captures `fn` (one step) in a HIP graph, checks a replay against the
+    eager result, then times `steps` replays with HIP events on the capture
+    stream (the stream every launch of the step is made on)."""
+
+    def __init__(self, torch, fn, check=None):
+        self.torch = torch
+        self.fn = fn
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            eager = fn()  # first call: scratch allocation happens here, outside capture
+            torch.cuda.synchronize()
+            eager = [t.clone() for t in eager] if eager else []
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=s):
+                self.outs = fn()
+        torch.cuda.current_stream().wait_stream(s)
+        self.stream = s
+        self.graph.replay()
+        torch.cuda.synchronize()
+        if eager:
+            for a, b in zip(eager, self.outs):
+                if not torch.equal(a, b):
+                    raise RuntimeError("graph replay differs from the eager step")
+
+    def time(self, steps: int, warmup: int) -> float:
+        torch = self.torch
+        for _ in range(warmup):
+            self.graph.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(self.stream):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            for _ in range(steps):
+                self.graph.replay()
+            e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps  # ms per step
+
+
+def rand_f16(torch, n, gen):
+    return torch.randn(n, generator=gen, device="cuda", dtype=torch.float32).to(torch.float16)
+
+
+def bench_decode_f16(torch, g, heads, kv, hd, tk, cap, scale_q, steps, warmup, layers, f32_cache=False):
+    from ttsxabe_amd.gpu import DecodeScratch
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    esz = 4 if f32_cache else 2
+    bytes_layer = 2 * kv * tk * hd * esz
+    L = rotate_layers(2 * kv * cap * hd * esz, layers)
+    if f32_cache:
+        ks = [torch.randn(kv * cap * hd, generator=gen, device="cuda") for _ in range(L)]
+        vs = [torch.randn(kv * cap * hd, generator=gen, device="cuda") for _ in range(L)]
+    else:
+        ks = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
+        vs = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
+    qs = [torch.randn(heads * hd, generator=gen, device="cuda") for _ in range(L)]
+    scratch = DecodeScratch()
+    fn_ = g.attn_decode if f32_cache else g.attn_decode_f16
+    scale = hd ** -0.5
+
+    def step():
+        return [fn_(qs[l], ks[l], vs[l], heads, kv, hd, tk, cap, scale, scale_q, scratch) for l in range(L)]
+
+    ms = Timer(torch, step).time(steps, warmup)
+    per_launch_us = ms * 1e3 / L
+    gbs = bytes_layer / (per_launch_us * 1e-6) / 1e9
+    return dict(layers=L, ms_per_step=ms, us_per_launch=per_launch_us, bytes_per_launch=bytes_layer, gbs=gbs,
+                frac=gbs / HBM_PEAK_GBS)
+
+
+def bench_prefill(torch, g, tq, heads, kv, hd, steps, warmup, layers):
+    gen = torch.Generator(device="cuda").manual_seed(99)
+    cap = tq
+    flop = 4 * hd * heads * (tq * (tq + 1) // 2)  # bench_flash.rs:107-112, causal
+    L = max(1, min(layers, rotate_layers(2 * kv * cap * hd * 2 + 2 * tq * heads * hd * 4, layers)))
+    qs = [torch.randn(tq * heads * hd, generator=gen, device="cuda") for _ in range(L)]
+    ks = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
+    vs = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
+    scale = hd ** -0.5
+
+    def step():
+        return [g.flash_attn_f16(qs[l], ks[l], vs[l], tq, 0, heads, kv, hd, cap, scale, True) for l in range(L)]
+
+    ms = Timer(torch, step).time(steps, warmup)
+    us = ms * 1e3 / L
+    tf = flop / (us * 1e-6) / 1e12
+    return dict(tq=tq, layers=L, us_per_launch=us, flop_per_launch=flop, tflops=tf, frac=tf / F16_PEAK_TFLOPS)
+
+
+def bench_encoder(torch, g, t, heads, hd, steps, warmup, layers):
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    d = heads * hd
+    flop = 4 * hd * heads * t * t  # non-causal
+    L = rotate_layers(t * 3 * d * 4, layers)
+    qkvs = [torch.randn(t * 3 * d, generator=gen, device="cuda") for _ in range(L)]
+    scale = hd ** -0.5
+
+    def step():
+        return [g.flash_attn_rows(qkvs[l], t, heads, hd, scale) for l in range(L)]
+
+    ms = Timer(torch, step).time(steps, warmup)
+    us = ms * 1e3 / L
+    tf = flop / (us * 1e-6) / 1e12
+    return dict(layers=L, us_per_launch=us, flop_per_launch=flop, tflops=tf, frac=tf / F16_PEAK_TFLOPS)
+
+
+def bench_q8_batch(torch, g, steps, warmup):
+    from ttsxabe_amd.gpu import DecodeScratch, KvCacheQ8
+    from tests import configs
+    nseq, heads, kv, hd, cap = 32, 32, 8, 128, 8192
+    tk = configs.c5_lengths(nseq=nseq)
+    bytes_layer = 2 * kv * (hd + 2 * hd // 32) * int(tk.sum())  # 272 * 8 * sum(tk)
+    L = max(2, math.ceil(2 * LLC_BYTES / bytes_layer))
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    caches = []
+    for _ in range(L):
+        c = KvCacheQ8(nseq, kv, hd, cap)
+        c.k_codes.copy_(torch.randint(-127, 128, c.k_codes.shape, generator=gen, device="cuda", dtype=torch.int8))
+        c.v_codes.copy_(torch.randint(-127, 128, c.v_codes.shape, generator=gen, device="cuda", dtype=torch.int8))
+        c.k_scales.copy_((torch.randn(c.k_scales.shape, generator=gen, device="cuda").abs() * 0.02).half())
+        c.v_scales.copy_((torch.randn(c.v_scales.shape, generator=gen, device="cuda").abs() * 0.02).half())
+        caches.append(c)
+    q = [torch.randn(nseq * heads * hd, generator=gen, device="cuda") for _ in range(L)]
+    tk_d = torch.from_numpy(tk).to("cuda")
+    slot_d = torch.arange(nseq, dtype=torch.int32, device="cuda")
+    scratch = DecodeScratch()
+
+    def step():
+        return [g.attn_decode_q8_batch(q[l], caches[l], tk_d, slot_d, cap, heads, hd ** -0.5, False, scratch)
+                for l in range(L)]
+
+    ms = Timer(torch, step).time(steps, warmup)
+    us = ms * 1e3 / L
+    gbs = bytes_layer / (us * 1e-6) / 1e9
+    return dict(layers=L, us_per_launch=us, bytes_per_launch=bytes_layer, sum_tk=int(tk.sum()), gbs=gbs,
+                frac=gbs / HBM_PEAK_GBS, tokens_per_s=nseq / (us * 1e-6))
+
+
+def cpu_baseline(seconds: float):
+    """The oracle's restatement of the reference's scalar decode chain
+    (crates/llmtie-cuda/tests/kernels.rs:2733-2780 over an f16 cache), on a
+    C2 layer-step, at 1 thread, repeated for about `seconds`."""
+    import numpy as np
+    import oracle
+    heads, kv, hd, tk = 32, 8, 128, 4096
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(heads * hd, dtype=np.float32)
+    k = oracle.f32_to_f16(rng.standard_normal(kv * tk * hd, dtype=np.float32))
+    v = oracle.f32_to_f16(rng.standard_normal(kv * tk * hd, dtype=np.float32))
+    bytes_layer = 2 * kv * tk * hd * 2
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.decode_f16(q, k, v, heads, kv, hd, tk, tk, hd ** -0.5, False, threads=1)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return dict(value=round(bytes_layer * n / el / 1e9, 4), unit="GB/s", cores=1, kind="port",
+                sample=f"{n} C2 decode layer-steps (32/8/128 GQA, 4096-position f16 cache) through the oracle's "
+                       f"scalar f32 chain, 1 thread, {el:.1f} s",
+                ms_per_layer_step=round(el / n * 1e3, 2))
+
+
+def cpu_c1(seconds=3.0):
+    """Config 1 (f32 causal MHA prefill 8/8/64, 128 tokens) on the CPU path."""
+    import oracle
+    from tests import configs
+    c = configs.c1_cpu()
+    flop = 4 * c["hd"] * c["heads"] * (c["t"] * (c["t"] + 1) // 2)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        oracle.prefill_f32(c["q"], c["k"], c["v"], c["t"], c["heads"], c["heads"], c["hd"], c["scale"], True, 1)
+        n += 1
+    el = time.perf_counter() - t0
+    return dict(gflops=round(flop * n / el / 1e9, 3), ms=round(el / n * 1e3, 3), threads=1)
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, calibrated)."""
+    p = ROOT / "profiles" / name
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU (--gpus > 1) is out of scope: attention "
+                                   "shards by head/sequence with no exchange, see DESIGN.md"}))
+        sys.exit(2)
+    import torch
+    from ttsxabe_amd.gpu import Gpu
+    g = Gpu(0)
+    print("bench: C2 decode", file=sys.stderr, flush=True)
+    c2 = bench_decode_f16(torch, g, 32, 8, 128, 4096, 4096, False, a.steps, a.warmup, a.layers)
+    line = {
+        "metric": "decode attn HBM GB/s + prefill attn TFLOP/s (% roofline), 1×MI355X",
+        "value": round(c2["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(c2["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) f16 KV caches, f32 queries)",
+        "config": {"workload": "C2: Llama-3-8B GQA decode, 32 q / 8 kv heads, head_dim 128, 4096-position f16 "
+                               "KV cache, batch 1; one step = one token through %d layers (distinct caches, "
+                               "HIP-graph replay)" % c2["layers"],
+                   "heads": 32, "kv_heads": 8, "head_dim": 128, "context": 4096, "layers": c2["layers"],
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(c2["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(c2["frac"], 4), "traffic": traffic_from_profiles("attn_decode_c2_counters.md"),
+                     "kernel": "attn_decode_kernel<128, KV_F16>", "bytes_per_launch": c2["bytes_per_launch"],
+                     "us_per_launch": round(c2["us_per_launch"], 3)},
+    }
+    if not a.no_secondary:
+        sec = {}
+        steps = max(5, a.steps // 2)
+        print("bench: C3 prefill", file=sys.stderr, flush=True)
+        for tq in (512, 128):
+            sec[f"c3_prefill_{tq}"] = bench_prefill(torch, g, tq, 32, 8, 128, steps, a.warmup, a.layers)
+        sec["c3_prefill_8192_steady"] = bench_prefill(torch, g, 8192, 32, 8, 128, max(3, steps // 5), 2, 1)
+        print("bench: C4", file=sys.stderr, flush=True)
+        sec["c4_encoder"] = bench_encoder(torch, g, 1500, 20, 64, steps, a.warmup, a.layers)
+        sec["c4_cross_decode"] = bench_decode_f16(torch, g, 20, 20, 64, 1500, 1500, True, steps, a.warmup,
+                                                  a.layers)
+        sec["c4_self_decode_224_f32"] = bench_decode_f16(torch, g, 20, 20, 64, 224, 448, True, steps, a.warmup,
+                                                         a.layers, f32_cache=True)
+        print("bench: C5", file=sys.stderr, flush=True)
+        sec["c5_q8_batch_decode"] = bench_q8_batch(torch, g, steps, a.warmup)
+        for v in sec.values():
+            for k2 in list(v):
+                if isinstance(v[k2], float):
+                    v[k2] = round(v[k2], 4)
+        line["secondary"] = sec
+    if not a.no_cpu:
+        print("bench: CPU baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
+        line["cpu_baseline"]["c1_cpu_prefill_f32"] = cpu_c1()
+        line["cpu_baseline"]["host_cpus"] = os.cpu_count()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -18,12 +18,14 @@
  *   q           [rows, heads * head_dim] f32, the heads of one GQA group adjacent
  *   K cache     [kv_heads, cap, head_dim]   (f32 or f16 bits)
  *   V cache     [kv_heads, head_dim, cap]   (transposed, f32 or f16 bits)
- *   Q8_0 cache  (new; no reference counterpart) for `slots` sequences:
- *     K codes   int8 [slots, kv_heads, cap, head_dim]
- *     V codes   int8 [slots, kv_heads, head_dim, cap]   (transposed)
- *     K, V scales f16 bits [slots, kv_heads, cap, head_dim / 32]
- *     element = f16 scale * int8 code, one scale per 32 dims of one position
- *     (the GGUF Q8_0 block, crates/llmtie-gguf/src/dequant.rs:180-185).
+ *   tiled f16   (new) one buffer per layer, [kv_heads][blocks of 32 positions],
+ *               each block K then V in MFMA fragment order (kvlayout.h)
+ *   Q8_0 cache  (new; no reference counterpart) for `slots` sequences, tiled the
+ *               same way: [slots][kv_heads][blocks], each block K codes, V
+ *               codes, K scales, V scales; element = f16 scale * int8 code, one
+ *               scale per 32 dims of one position (the GGUF Q8_0 block,
+ *               crates/llmtie-gguf/src/dequant.rs:180-185); 272 bytes per
+ *               position and kv head at head_dim 128.
  *   int8 twin   `n` int8 codes then `n / 32` f32 scales in one buffer (the
  *               reference's `Q8` buffer, device.rs:498-520)
  */
@@ -126,20 +128,68 @@ int llmtie_attn_decode(void* stream, const float* q, size_t q_len, const float* 
                        size_t v_len, size_t heads, size_t kv_heads, size_t head_dim, size_t tk, size_t cap,
                        float scale, int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len);
 
-/* Batched decode over a GGUF Q8_0 cache (new; the reference's nearest caller
- * is Translator::step_rows, crates/llmtie-translate/src/model.rs:764, which
- * launches one f16 decode per row). nseq sequences in one launch: sequence s
- * attends its tk_dev[s] live positions of cache slot slot_dev[s]; q and out
- * are [nseq, heads*head_dim]. tk_dev and slot_dev are device int32 arrays;
- * max_tk bounds every tk_dev[s] (the kernel clamps to it, never reading past
- * it) and must be <= cap. A sequence whose slot is out of range or whose
- * length is 0 gets a NaN row. cap must be a multiple of 32. */
-int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, const int8_t* k_codes,
-                                const uint16_t* k_scales, const int8_t* v_codes, const uint16_t* v_scales,
+/* Batched decode over a tiled GGUF Q8_0 cache (new; the reference's nearest
+ * caller is Translator::step_rows, crates/llmtie-translate/src/model.rs:764,
+ * which launches one f16 decode per row). nseq sequences in one launch:
+ * sequence s attends its tk_dev[s] live positions of cache slot slot_dev[s];
+ * q and out are [nseq, heads*head_dim]. tk_dev and slot_dev are device int32
+ * arrays; max_tk bounds every tk_dev[s] (the kernel clamps to it, never
+ * reading past it) and must be <= cap. A sequence whose slot is out of range
+ * or whose length is 0 gets a NaN row. cache_len is in bytes
+ * (llmtie_q8_cache_bytes). */
+int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, const int8_t* cache, size_t cache_len,
                                 size_t slots, const int32_t* tk_dev, const int32_t* slot_dev, size_t nseq,
                                 size_t max_tk, size_t heads, size_t kv_heads, size_t head_dim, size_t cap,
                                 float scale, int scale_q, llmtie_decode_scratch* scratch, float* out,
                                 size_t out_len);
+
+/* ------------------------------------------- tiled f16 cache (new layout)
+ *
+ * One buffer per layer holds K and V in fragment order, 32 positions a block
+ * (see ttsxabe_amd/csrc/kvlayout.h): every load the decode and prefill kernels
+ * make of it is a contiguous 1 KB wave-wide read. These mirror the reference
+ * operators they are named after, with the two cache slices replaced by the
+ * one tiled buffer; cap may be any positive count (rounded up to whole blocks
+ * internally). */
+
+/* Halves a tiled f16 cache of this shape holds. */
+size_t llmtie_t16_cache_len(size_t kv_heads, size_t head_dim, size_t cap);
+
+/* cache_append_f16 (device.rs:2849) into the tiled cache; value selects V. */
+int llmtie_t16_append(void* stream, const float* src, size_t src_len, size_t src_off, uint16_t* cache,
+                      size_t cache_len, size_t n, size_t kv_heads, size_t head_dim, size_t cap, size_t past,
+                      int value);
+
+/* rope_cache_f16 (device.rs:2915) into the tiled cache. */
+int llmtie_t16_rope_cache(void* stream, float* q, size_t q_len, size_t q_off, const float* k, size_t k_len,
+                          size_t k_off, const float* v, size_t v_len, size_t v_off, const float* freq_div,
+                          size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, uint16_t* cache,
+                          size_t cache_len, size_t cap);
+
+/* cache_grow_f16 (device.rs:3152) for the tiled cache. */
+int llmtie_t16_grow(void* stream, const uint16_t* src, size_t src_len, uint16_t* dst, size_t dst_len,
+                    size_t kv_heads, size_t head_dim, size_t cap, size_t new_cap, size_t live);
+
+/* Repack reference-layout f16 caches (positions 0..live-1) into a tiled one. */
+int llmtie_t16_from_ref(void* stream, const uint16_t* k, size_t k_len, const uint16_t* v, size_t v_len,
+                        size_t kv_heads, size_t head_dim, size_t cap, size_t live, uint16_t* cache,
+                        size_t cache_len);
+
+/* attn_decode_f16 (device.rs:5949) off the tiled cache. */
+int llmtie_attn_decode_t16(void* stream, const float* q, size_t q_len, const uint16_t* cache, size_t cache_len,
+                           size_t heads, size_t kv_heads, size_t head_dim, size_t tk, size_t cap, float scale,
+                           int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len);
+
+/* attn_decode_f16_q_row (device.rs:6001) off the tiled cache; twin may be NULL. */
+int llmtie_attn_decode_t16_q_row(void* stream, const float* q, size_t q_len, size_t q_off, const uint16_t* cache,
+                                 size_t cache_len, size_t heads, size_t kv_heads, size_t head_dim, size_t tk,
+                                 size_t cap, float scale, int scale_q, llmtie_decode_scratch* scratch, float* out,
+                                 size_t out_len, int8_t* twin, size_t twin_rows, size_t twin_k, size_t row);
+
+/* flash_attn_f16 (device.rs:5754) off the tiled cache. */
+int llmtie_flash_attn_t16(void* stream, const float* q, size_t q_len, const uint16_t* cache, size_t cache_len,
+                          float* out, size_t out_len, size_t tq, size_t past, size_t heads, size_t kv_heads,
+                          size_t head_dim, size_t cap, float scale, int causal);
 
 /* --------------------------------------------------------- KV producers */
 
@@ -172,21 +222,22 @@ int llmtie_cache_grow_f16(void* stream, const uint16_t* src, size_t src_len, uin
                           size_t kv_heads, size_t head_dim, size_t cap, size_t new_cap, size_t live,
                           int transposed);
 
+/* Bytes a tiled Q8_0 cache of this shape holds (layout at the top). */
+size_t llmtie_q8_cache_bytes(size_t slots, size_t kv_heads, size_t head_dim, size_t cap);
+
 /* Q8_0 cache append (new): n rows of k[k_off..] and v[v_off..] ([n,
  * kv_heads*head_dim], k already rotated) quantized into slot `slot` at
  * positions past.. . Quantization is ggml's quantize_row_q8_0_ref. */
 int llmtie_kv_q8_append(void* stream, const float* k, size_t k_len, size_t k_off, const float* v, size_t v_len,
-                        size_t v_off, int8_t* k_codes, uint16_t* k_scales, int8_t* v_codes, uint16_t* v_scales,
-                        size_t slots, size_t slot, size_t n, size_t kv_heads, size_t head_dim, size_t cap,
-                        size_t past);
+                        size_t v_off, int8_t* cache, size_t cache_len, size_t slots, size_t slot, size_t n,
+                        size_t kv_heads, size_t head_dim, size_t cap, size_t past);
 
 /* The Q8_0 twin of llmtie_rope_cache_f16 (new): q rotated in place, k rotated
  * and quantized, v quantized, into slot `slot` at `pos`. */
 int llmtie_rope_cache_q8(void* stream, float* q, size_t q_len, size_t q_off, const float* k, size_t k_len,
                          size_t k_off, const float* v, size_t v_len, size_t v_off, const float* freq_div,
-                         size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, int8_t* k_codes,
-                         uint16_t* k_scales, int8_t* v_codes, uint16_t* v_scales, size_t slots, size_t slot,
-                         size_t cap);
+                         size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, int8_t* cache,
+                         size_t cache_len, size_t slots, size_t slot, size_t cap);
 
 #ifdef __cplusplus
 }

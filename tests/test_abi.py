@@ -1,0 +1,100 @@
+"""The C ABI as a library: it loads, exports every function include/llmtie_hip.h
+declares with the argument count the host binding uses, and refuses shapes
+before touching a device (the reference's refusals, error.rs:148-282), so all
+of this runs on a machine with no GPU."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from ttsxabe_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "llmtie_hip.h"
+
+
+def declared():
+    """name -> argument count, parsed from the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|void|size_t|const char\*|llmtie_decode_scratch\*)\s+(llmtie_\w+)\s*\(([^)]*)\)\s*;",
+                         text):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_header_and_binding_agree():
+    d = declared()
+    assert len(d) >= 30
+    assert set(d) == set(_lib.SIGNATURES), set(d) ^ set(_lib.SIGNATURES)
+    for name, n in d.items():
+        assert len(_lib.SIGNATURES[name][1]) == n, name
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared():
+        assert hasattr(L, name), name
+    assert L.llmtie_version() == b"0.1.0"
+
+
+def last():
+    e = _lib.LlmtieError()
+    _lib.lib().llmtie_last_error(C.byref(e))
+    return e
+
+
+NULL = None
+
+
+def test_supports_flash_is_the_reference_predicate():
+    L = _lib.lib()
+    assert L.llmtie_supports_flash(128, 32, 8)
+    assert L.llmtie_supports_flash(64, 20, 20)
+    assert not L.llmtie_supports_flash(96, 4, 4)
+    assert not L.llmtie_supports_flash(128, 4, 3)
+
+
+def test_refusals_happen_before_any_launch():
+    L = _lib.lib()
+    # An uninstantiated head width (kernels.rs tests :2442-2473).
+    assert L.llmtie_flash_attn(NULL, NULL, 10**9, NULL, 10**9, NULL, 10**9, NULL, 10**9, 4, 0, 4, 4, 96, 4,
+                               C.c_float(1.0), 0) == 1
+    e = last()
+    assert e.status == 1 and list(e.field)[:3] == [96, 4, 4]
+    assert b"head_dim 96" in e.message
+    # An odd f16 capacity.
+    assert L.llmtie_flash_attn_f16(NULL, NULL, 10**9, NULL, 10**9, NULL, 10**9, NULL, 10**9, 4, 0, 4, 4, 128, 7,
+                                   C.c_float(1.0), 1) == 2
+    # More keys than the cache holds; no keys at all (kernels.rs:2905-2937).
+    for tk in (257, 0):
+        assert L.llmtie_attn_decode_f16(NULL, NULL, 10**9, NULL, 10**9, NULL, 10**9, 8, 2, 128, tk, 256,
+                                        C.c_float(1.0), 0, NULL, NULL, 10**9) == 3
+    # A group wider than the 16 columns of the kernel's tile.
+    assert L.llmtie_attn_decode_f16(NULL, NULL, 10**9, NULL, 10**9, NULL, 10**9, 34, 2, 128, 10, 256,
+                                    C.c_float(1.0), 0, NULL, NULL, 10**9) == 1
+    # A short cache slice.
+    assert L.llmtie_attn_decode_f16(NULL, NULL, 10**9, NULL, 100, NULL, 10**9, 8, 2, 128, 10, 256,
+                                    C.c_float(1.0), 0, NULL, NULL, 10**9) == 4
+    assert list(last().field)[:2] == [2 * 256 * 128, 100]
+    # A twin of the wrong shape (device.rs:6362-6372).
+    assert L.llmtie_attn_decode_f16_q_row(NULL, NULL, 10**9, 0, NULL, 10**9, NULL, 10**9, 8, 8, 128, 37, 64,
+                                          C.c_float(0.1), 0, NULL, NULL, 10**9, NULL, 1, 1024, 1) == 6
+    # A rope reading past the end (kernels.rs:2212-2240), an odd rotary head.
+    assert L.llmtie_rope(NULL, NULL, 32, 1, NULL, 2, 2, 8, C.c_float(1e4), 0) == 4
+    assert L.llmtie_rope(NULL, NULL, 10**6, 0, NULL, 2, 2, 7, C.c_float(1e4), 0) == 7
+    # Growth that shrinks or overruns.
+    assert L.llmtie_cache_grow(NULL, NULL, 10**6, NULL, 10**6, 2, 4, 8, 16, 9, 0) == 3
+    assert L.llmtie_cache_grow(NULL, NULL, 10**6, NULL, 10**6, 2, 4, 16, 8, 4, 0) == 3
+    # Null buffers with valid shapes are refused rather than dereferenced.
+    assert L.llmtie_cache_append(NULL, NULL, 100, 0, NULL, 1000, 1, 2, 8, 8, 0, 0) == 10
+
+
+def test_q8_and_tiled_sizes():
+    L = _lib.lib()
+    # 272 bytes per position and kv head at head_dim 128, whole 32-position blocks.
+    assert L.llmtie_q8_cache_bytes(1, 1, 128, 32) == 272 * 32
+    assert L.llmtie_q8_cache_bytes(2, 8, 128, 33) == 2 * 8 * 2 * 272 * 32
+    assert L.llmtie_t16_cache_len(8, 128, 4096) == 8 * 4096 * 128 * 2
+    assert L.llmtie_t16_cache_len(20, 64, 1500) == 20 * 47 * 32 * 64 * 2

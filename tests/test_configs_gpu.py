@@ -38,6 +38,11 @@ def test_c2_llama3_gqa_decode(gpu):
     got = down(gpu.attn_decode_f16(up(c["q"]), dk, dv, c["heads"], c["kv"], c["hd"], c["tk"], c["cap"], c["scale"],
                                    False, DecodeScratch()))
     check(want, got, 1, c["heads"], c["hd"], "C2 decode")
+    from ttsxabe_amd.gpu import TiledCache16
+    t = TiledCache16(c["kv"], c["hd"], c["cap"])
+    gpu.t16_from_ref(dk, dv, t, c["tk"])
+    got_t = down(gpu.attn_decode_t16(up(c["q"]), t, c["heads"], c["tk"], c["scale"], False, DecodeScratch()))
+    check(want, got_t, 1, c["heads"], c["hd"], "C2 decode (tiled cache)")
 
 
 @pytest.mark.parametrize("tq", [128, 512])
@@ -54,6 +59,11 @@ def test_c3_llama3_gqa_prefill(gpu, tq):
     tol = 2e-4 + 1e-2 * np.abs(want) + 1e-2 * spread
     assert (np.abs(want - got) <= tol).all()
     check(want, got, tq, c["heads"], c["hd"], f"C3 prefill {tq}")
+    from ttsxabe_amd.gpu import TiledCache16
+    t = TiledCache16(c["kv"], c["hd"], c["cap"])
+    gpu.t16_from_ref(dk, dv, t, tq)
+    got_t = down(gpu.flash_attn_t16(up(c["q"]), t, tq, 0, c["heads"], c["scale"], True)).astype(np.float64)
+    assert np.array_equal(got, got_t), "tiled-cache prefill differs from the reference-layout one"
 
 
 def test_c4_whisper_encoder(gpu):
@@ -94,11 +104,10 @@ def test_c4_whisper_cross_and_self_decode(gpu):
 def test_c5_batched_q8_decode(gpu):
     from ttsxabe_amd.gpu import DecodeScratch, KvCacheQ8
     c = configs.c5_q8()
+    from tests import tiled
     cache = KvCacheQ8(c["slots"], c["kv"], c["hd"], c["cap"])
-    cache.k_codes.copy_(torch.from_numpy(c["kc"]))
-    cache.v_codes.copy_(torch.from_numpy(c["vc"]))
-    cache.k_scales.copy_(torch.from_numpy(c["ks"].view(np.float16)))
-    cache.v_scales.copy_(torch.from_numpy(c["vs"].view(np.float16)))
+    cache.data.copy_(torch.from_numpy(tiled.pack_q8(c["kc"], c["ks"], c["vc"], c["vs"], c["slots"], c["kv"], c["hd"],
+                                                    c["cap"])))
     got = down(gpu.attn_decode_q8_batch(up(c["q"]), cache, up(c["tk"], torch.int32), up(c["slot"], torch.int32),
                                         c["cap"], c["heads"], c["scale"], False, DecodeScratch()))
     want = oracle.decode_q8_batch(c["q"], c["kc"], c["ks"], c["vc"], c["vs"], c["tk"], c["slot"], c["heads"],

@@ -61,6 +61,14 @@ def test_the_fused_decode_attention_matches_the_chain(gpu, i):
     a = down(f(dq, dk, dv, heads, kv, hd, tk, cap, scale, scale_q, scratch))
     b = down(f(dq, dk, dv, heads, kv, hd, tk, cap, scale, scale_q, scratch))
     assert np.array_equal(a, b), "not reproducible through one scratch"
+    if half:
+        # The tiled cache holds the same halves in fragment order: the same
+        # MFMA inputs in the same slots, so the same bits out.
+        from ttsxabe_amd.gpu import TiledCache16
+        t = TiledCache16(kv, hd, cap)
+        gpu.t16_from_ref(dk, dv, t, tk)
+        c_ = down(gpu.attn_decode_t16(dq, t, heads, tk, scale, scale_q, scratch))
+        assert np.array_equal(a, c_), "tiled cache differs from the reference layout"
     exact = oracle.decode_f64(q, k, v, heads, kv, hd, tk, cap, scale, scale_q)
     own = full_scale_err(exact, want)  # the f32 chain's own rounding
     err_exact = full_scale_err(exact, a)
@@ -134,3 +142,24 @@ def test_the_decode_attention_into_a_row_is_the_decode_attention(gpu):
     short = gpu.q8_zeros(1, n)
     with pytest.raises(MismatchedQ8):
         gpu.attn_decode_f16_q_row(up(qs), row * n, dk, dv, heads, kv, hd, tk, cap, 0.1, False, s, out, short, row)
+
+
+def test_one_scratch_serves_alternating_inputs(gpu):
+    """Partials handed between workgroups must never be read stale: two
+    different queries and caches alternate through one scratch, each call
+    checked against the chain (a stale partial would carry the other call's
+    numbers, which a same-input repeat cannot show)."""
+    from ttsxabe_amd.gpu import DecodeScratch
+    heads, kv, hd, tk, cap = 32, 8, 128, 4096, 4096
+    s = DecodeScratch()
+    cases = []
+    for salt in (700, 710):
+        q = oracle.seq(heads * hd, salt)
+        k = oracle.through_f16(oracle.seq(kv * cap * hd, salt + 1))
+        v = oracle.through_f16(oracle.seq(kv * hd * cap, salt + 2))
+        exact = oracle.decode_f64(q, k, v, heads, kv, hd, tk, cap, 0.11)
+        cases.append((up(q), up_f16(k), up_f16(v), exact))
+    for rep in range(6):
+        q, k, v, exact = cases[rep % 2]
+        got = down(gpu.attn_decode_f16(q, k, v, heads, kv, hd, tk, cap, 0.11, False, s))
+        assert full_scale_err(exact, got) < 2e-5, f"call {rep}"

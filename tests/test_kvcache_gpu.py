@@ -11,6 +11,7 @@ import pytest
 import torch
 
 import oracle
+from tests import tiled
 from tests.util import down, full_scale_err, up, up_f16
 
 pytestmark = pytest.mark.gpu
@@ -121,12 +122,9 @@ def test_an_offset_past_the_end_of_the_source_is_refused(gpu):
         gpu.cache_append(x, 1, dst, t, heads, hd, 8, 0, False)
 
 
-def _q8_views(cache):
-    kc = down(cache.k_codes)
-    vc = down(cache.v_codes)
-    ks = down(cache.k_scales).view(np.uint16)
-    vs = down(cache.v_scales).view(np.uint16)
-    return kc, ks, vc, vs
+def _plain_q8(slots, kv, hd, cap):
+    n = slots * kv * cap * hd
+    return (np.zeros(n, np.int8), np.zeros(n // 32, np.uint16), np.zeros(n, np.int8), np.zeros(n // 32, np.uint16))
 
 
 @pytest.mark.parametrize("hd", [64, 128])
@@ -139,24 +137,22 @@ def test_q8_append_is_ggml_quantize(gpu, hd):
     k[:32] = 0.0  # an all-zero block: scale 0, codes 0
     v[5] = 127.0 * 0.5 / 10.0  # a value sitting near a rounding tie
     gpu.kv_q8_append(up(k), 0, up(v), 0, cache, slot, n, past)
-    kc, ks, vc, vs = _q8_views(cache)
-    nb = hd // 32
+    kc, ks, vc, vs = _plain_q8(slots, kv, hd, cap)
+    kc4 = kc.reshape(slots, kv, cap, hd)
+    vc4 = vc.reshape(slots, kv, hd, cap)
+    ks4 = ks.reshape(slots, kv, cap, hd // 32)
+    vs4 = vs.reshape(slots, kv, cap, hd // 32)
     for t in range(n):
         for h in range(kv):
             row = (t * kv + h) * hd
-            wc, wsc = oracle.q8_0_quantize(k[row:row + hd])
-            kvh = slot * kv + h
-            at = (kvh * cap + past + t)
-            assert np.array_equal(kc[at * hd:(at + 1) * hd], wc)
-            assert np.array_equal(ks[at * nb:(at + 1) * nb], wsc)
-            wc, wsc = oracle.q8_0_quantize(v[row:row + hd])
-            got = vc.reshape(slots * kv, hd, cap)[kvh, :, past + t]
-            assert np.array_equal(got, wc)
-            assert np.array_equal(vs[at * nb:(at + 1) * nb], wsc)
-    # Nothing outside the written positions moved.
-    mask = np.zeros((slots * kv, cap), bool)
-    mask[slot * kv:(slot + 1) * kv, past:past + n] = True
-    assert (kc.reshape(slots * kv, cap, hd)[~mask] == 0).all()
+            c, sc = oracle.q8_0_quantize(k[row:row + hd])
+            kc4[slot, h, past + t] = c
+            ks4[slot, h, past + t] = sc
+            c, sc = oracle.q8_0_quantize(v[row:row + hd])
+            vc4[slot, h, :, past + t] = c
+            vs4[slot, h, past + t] = sc
+    want = tiled.pack_q8(kc, ks, vc, vs, slots, kv, hd, cap)
+    assert np.array_equal(down(cache.data), want)
 
 
 def test_the_q8_rotate_and_cache_is_rope_then_q8_append(gpu):
@@ -176,5 +172,50 @@ def test_the_q8_rotate_and_cache_is_rope_then_q8_append(gpu):
     qb = up(q)
     gpu.rope_cache_q8(qb, 0, up(k), 0, up(v), 0, div, heads, theta, pos, b, slot)
     assert torch.equal(qa, qb)
-    for x, y in zip(_q8_views(a), _q8_views(b)):
-        assert np.array_equal(x, y)
+    assert torch.equal(a.data, b.data)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_tiled_f16_producers_are_the_reference_producers_repacked(gpu, hd):
+    """t16_append / t16_rope_cache / t16_from_ref write exactly the reference
+    layout's bits, repacked as the numpy packer says; t16_grow re-strides."""
+    from ttsxabe_amd.gpu import TiledCache16
+    heads, kv, cap, n, past = 8, 2, 100, 37, 3
+    theta = 500000.0
+    src_k = up(oracle.seq(n * kv * hd, 51))
+    src_v = up(oracle.seq(n * kv * hd, 52))
+    rk = torch.zeros(kv * cap * hd, dtype=torch.float16, device="cuda")
+    rv = torch.zeros(kv * cap * hd, dtype=torch.float16, device="cuda")
+    gpu.cache_append_f16(src_k, 0, rk, n, kv, hd, cap, past, False)
+    gpu.cache_append_f16(src_v, 0, rv, n, kv, hd, cap, past, True)
+    t = TiledCache16(kv, hd, cap)
+    gpu.t16_append(src_k, 0, t, n, past, False)
+    gpu.t16_append(src_v, 0, t, n, past, True)
+    want = tiled.pack_t16(down(rk).view(np.uint16), down(rv).view(np.uint16), kv, hd, cap)
+    assert np.array_equal(down(t.data).view(np.uint16), want)
+    # The device repacker agrees with the numpy packer.
+    t2 = TiledCache16(kv, hd, cap)
+    gpu.t16_from_ref(rk, rv, t2, past + n)
+    assert torch.equal(t.data, t2.data)
+    # Fused rotate + cache at one position.
+    q = oracle.seq(heads * hd, 53)
+    kx = oracle.seq(kv * hd, 54)
+    vx = oracle.seq(kv * hd, 55)
+    qa, qb = up(q), up(q)
+    gpu.rope_cache_f16(qa, 0, up(kx), 0, up(vx), 0, None, heads, kv, hd, theta, past + n, rk, rv, cap)
+    gpu.t16_rope_cache(qb, 0, up(kx), 0, up(vx), 0, None, heads, theta, past + n, t)
+    assert torch.equal(qa, qb)
+    want = tiled.pack_t16(down(rk).view(np.uint16), down(rv).view(np.uint16), kv, hd, cap)
+    assert np.array_equal(down(t.data).view(np.uint16), want)
+    # Growth: every head's blocks land where the larger capacity wants them.
+    big = TiledCache16(kv, hd, 2 * cap)
+    gpu.t16_grow(t, big, past + n + 1)
+    rk2 = torch.zeros(kv * 2 * cap * hd, dtype=torch.float16, device="cuda")
+    rv2 = torch.zeros(kv * 2 * cap * hd, dtype=torch.float16, device="cuda")
+    gpu.cache_grow_f16(rk, rk2, kv, hd, cap, 2 * cap, past + n + 1, False)
+    gpu.cache_grow_f16(rv, rv2, kv, hd, cap, 2 * cap, past + n + 1, True)
+    want = tiled.pack_t16(down(rk2).view(np.uint16), down(rv2).view(np.uint16), kv, hd, 2 * cap, live=past + n + 1)
+    got = down(big.data).view(np.uint16)
+    # Positions past `live` inside the last copied block are carried along
+    # whole (they were zero in the source), so the images agree everywhere.
+    assert np.array_equal(got, want)

@@ -34,6 +34,12 @@ def fused_attention_sized(gpu, heads, kv, hd, causal, tq, past, cap, half):
     kc, vc = caches(oracle.seq(kv * tk * hd, 72), oracle.seq(kv * tk * hd, 73), kv, tk, cap, hd)
     if half:
         out = gpu.flash_attn_f16(up(q), up_f16(kc), up_f16(vc), tq, past, heads, kv, hd, cap, scale, causal)
+        from ttsxabe_amd.gpu import TiledCache16
+        t = TiledCache16(kv, hd, cap, zero=False)  # garbage past tk must not leak in
+        t.data.fill_(float("nan"))
+        gpu.t16_from_ref(up_f16(kc), up_f16(vc), t, tk)
+        out_t = gpu.flash_attn_t16(up(q), t, tq, past, heads, scale, causal)
+        assert torch.equal(out, out_t), "tiled-cache prefill differs from the reference-layout one"
     else:
         out = gpu.flash_attn(up(q), up(kc), up(vc), tq, past, heads, kv, hd, cap, scale, causal)
     got = down(out).astype(np.float64)

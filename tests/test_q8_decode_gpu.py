@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import oracle
+from tests import tiled
 from tests.util import down, full_scale_err, up
 
 pytestmark = pytest.mark.gpu
@@ -25,10 +26,8 @@ def random_q8_cache(slots, kv, hd, cap, seed):
 
 
 def load(cache, kc, ks, vc, vs):
-    cache.k_codes.copy_(torch.from_numpy(kc))
-    cache.v_codes.copy_(torch.from_numpy(vc))
-    cache.k_scales.copy_(torch.from_numpy(ks.view(np.float16)))
-    cache.v_scales.copy_(torch.from_numpy(vs.view(np.float16)))
+    packed = tiled.pack_q8(kc, ks, vc, vs, cache.slots, cache.kv_heads, cache.head_dim, cache.cap)
+    cache.data.copy_(torch.from_numpy(packed))
 
 
 def dequant_seq(kc, ks, vc, vs, slot, kv, hd, cap):
@@ -68,8 +67,10 @@ def test_batched_q8_decode_matches_the_chain_on_the_dequantised_cache(gpu, hd, h
         chain = want[i * n:(i + 1) * n]
         own = full_scale_err(exact, chain)
         g = got1[i * n:(i + 1) * n]
-        assert full_scale_err(exact, g) < 2e-5, f"seq {i}"
-        assert full_scale_err(chain, g) < 2e-5 + own, f"seq {i}"
+        # One f16 rounding of P * d_v on the value side (about 2^-12 of full
+        # scale), far inside the 8-bit quantisation of the cache itself.
+        assert full_scale_err(exact, g) < 1e-3, f"seq {i}"
+        assert full_scale_err(chain, g) < 1e-3 + own, f"seq {i}"
 
 
 def test_a_mis_described_sequence_gets_nan_and_its_neighbours_do_not(gpu):
@@ -96,6 +97,8 @@ def test_q8_refusals(gpu):
         gpu.attn_decode_q8_batch(q, cache, tk, tk * 0, 65, 8, 0.1, False, s)
     with pytest.raises(UnsupportedAttention):
         gpu.attn_decode_q8_batch(q, cache, tk, tk * 0, 64, 7, 0.1, False, s)
-    bad = KvCacheQ8(1, 2, 128, 48)
-    with pytest.raises(RaggedBlock):
-        gpu.attn_decode_q8_batch(q, bad, tk, tk * 0, 10, 8, 0.1, False, s)
+    short = KvCacheQ8(1, 2, 128, 64)
+    short.data = short.data[:100]
+    from ttsxabe_amd.gpu import SliceOverrun
+    with pytest.raises(SliceOverrun):
+        gpu.attn_decode_q8_batch(q, short, tk, tk * 0, 10, 8, 0.1, False, s)

@@ -39,16 +39,24 @@ SIGNATURES = {
     "llmtie_attn_decode_f16_q_row": (I, [P, P, SZ, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ, P, SZ,
                                          SZ, SZ]),
     "llmtie_attn_decode": (I, [P, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ]),
-    "llmtie_attn_decode_q8_batch": (I, [P, P, SZ, P, P, P, P, SZ, P, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ]),
+    "llmtie_attn_decode_q8_batch": (I, [P, P, SZ, P, SZ, SZ, P, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ]),
+    "llmtie_t16_cache_len": (SZ, [SZ, SZ, SZ]),
+    "llmtie_t16_append": (I, [P, P, SZ, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, I]),
+    "llmtie_t16_rope_cache": (I, [P, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, SZ, F, SZ, P, SZ, SZ]),
+    "llmtie_t16_grow": (I, [P, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ]),
+    "llmtie_t16_from_ref": (I, [P, P, SZ, P, SZ, SZ, SZ, SZ, SZ, P, SZ]),
+    "llmtie_attn_decode_t16": (I, [P, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ]),
+    "llmtie_attn_decode_t16_q_row": (I, [P, P, SZ, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ, P, SZ, SZ, SZ]),
+    "llmtie_flash_attn_t16": (I, [P, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, SZ, F, I]),
     "llmtie_rope": (I, [P, P, SZ, SZ, P, SZ, SZ, SZ, F, SZ]),
     "llmtie_cache_append": (I, [P, P, SZ, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, I]),
     "llmtie_cache_append_f16": (I, [P, P, SZ, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, I]),
     "llmtie_rope_cache_f16": (I, [P, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, SZ, F, SZ, P, P, SZ, SZ]),
     "llmtie_cache_grow": (I, [P, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, I]),
     "llmtie_cache_grow_f16": (I, [P, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, I]),
-    "llmtie_kv_q8_append": (I, [P, P, SZ, SZ, P, SZ, SZ, P, P, P, P, SZ, SZ, SZ, SZ, SZ, SZ, SZ]),
-    "llmtie_rope_cache_q8": (I, [P, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, SZ, F, SZ, P, P, P, P, SZ, SZ,
-                                 SZ]),
+    "llmtie_q8_cache_bytes": (SZ, [SZ, SZ, SZ, SZ]),
+    "llmtie_kv_q8_append": (I, [P, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, SZ, SZ]),
+    "llmtie_rope_cache_q8": (I, [P, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, SZ, F, SZ, P, SZ, SZ, SZ, SZ]),
 }
 
 _lib = None

@@ -12,6 +12,7 @@
 
 #include "../../include/llmtie_hip.h"
 #include "decode.h"
+#include "kvlayout.h"
 #include "kvcache.h"
 #include "prefill.h"
 
@@ -157,7 +158,8 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
 
 // Splits of one head: about `target` workgroups over the whole launch, each
 // wave taking whole 32-key blocks, and never more than the merge can hold.
-void plan_decode(size_t tk_max, size_t units, int& nit, int& splits) {
+void plan_decode(size_t tk_max, size_t units, size_t group, int& nit, int& splits) {
+    const size_t max_splits = std::min<size_t>(DECODE_MAX_SPLITS, DECODE_MAX_SPLIT_ROWS / std::max<size_t>(1, group));
     size_t target = 512;
     if (const char* e = getenv("LLMTIE_DECODE_WGS")) target = std::max(1, atoi(e));
     const size_t blocks = (tk_max + 31) / 32;
@@ -166,7 +168,7 @@ void plan_decode(size_t tk_max, size_t units, int& nit, int& splits) {
     size_t n = std::max<size_t>(1, (per_wg + 3) / 4);     // per wave
     if (const char* e = getenv("LLMTIE_DECODE_NIT")) n = std::max(1, atoi(e));
     size_t span = 4 * n * 32;
-    while ((tk_max + span - 1) / span > (size_t)DECODE_MAX_SPLITS) {
+    while ((tk_max + span - 1) / span > max_splits) {
         ++n;
         span = 4 * n * 32;
     }
@@ -218,14 +220,21 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
                   const void* v, size_t v_len, size_t heads, size_t kv_heads, size_t hd, size_t tk, size_t cap,
                   float scale, int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len,
                   size_t out_off, int8_t* twin, size_t twin_rows, size_t twin_k, bool has_twin) {
+    const bool tiled = kind == KV_T16;
     if (!(hd == 64 || hd == 128)) return unsupported(hd, heads, kv_heads);
     if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 16) return unsupported(hd, heads, kv_heads);
     if (tk == 0 || tk > cap) return overrun_cache(tk, cap);
     const size_t esz = kind == KV_F32 ? 4 : 2;
-    if ((cap * esz) % 8 != 0) return odd_cap(cap);
+    if (!tiled && (cap * esz) % 8 != 0) return odd_cap(cap);
     if (cap > IMAX || kv_heads * cap * hd > ((size_t)1 << 40)) return overrun_slice(kv_heads * cap * hd, IMAX);
-    const size_t need = kv_heads * cap * hd;
-    if (k_len < need || v_len < need) return overrun_slice(need, std::min(k_len, v_len));
+    if (tiled) {
+        const size_t need = kv_heads * (size_t)tiled_nblk((int)cap) * 64 * hd;
+        if (k_len < need) return overrun_slice(need, k_len);
+        v = k;
+    } else {
+        const size_t need = kv_heads * cap * hd;
+        if (k_len < need || v_len < need) return overrun_slice(need, std::min(k_len, v_len));
+    }
     const size_t n = heads * hd;
     if (q_len < q_off + n) return overrun_slice(q_off + n, q_len);
     if (out_len < out_off + n) return overrun_slice(out_off + n, out_len);
@@ -241,8 +250,9 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     if (!scratch) return invalid("scratch");
     const size_t group = heads / kv_heads;
     int nit, splits;
-    plan_decode(tk, kv_heads, nit, splits);
+    plan_decode(tk, kv_heads, group, nit, splits);
     const size_t part = kv_heads * (size_t)splits * group * (hd + 2);
+    const long ml_off = (long)(kv_heads * (size_t)splits * group * hd);
     int r = ensure_scratch(scratch, part, kv_heads, S(stream));
     if (r != LLMTIE_OK) return r;
     DecodeArgs a;
@@ -256,6 +266,7 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
         a.twin_scales = reinterpret_cast<float*>(twin + twin_rows * twin_k);
     }
     a.part = scratch->part;
+    a.ml_off = ml_off;
     a.ctr = scratch->ctr;
     a.q_off = (long)q_off;
     a.out_off = (long)out_off;
@@ -355,38 +366,37 @@ int llmtie_attn_decode(void* stream, const float* q, size_t q_len, const float* 
                          scale_q, scratch, out, out_len, 0, nullptr, 0, 0, false);
 }
 
-int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, const int8_t* k_codes,
-                                const uint16_t* k_scales, const int8_t* v_codes, const uint16_t* v_scales,
+int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, const int8_t* cache, size_t cache_len,
                                 size_t slots, const int32_t* tk_dev, const int32_t* slot_dev, size_t nseq,
                                 size_t max_tk, size_t heads, size_t kv_heads, size_t head_dim, size_t cap,
                                 float scale, int scale_q, llmtie_decode_scratch* scratch, float* out,
                                 size_t out_len) {
     if (!(head_dim == 64 || head_dim == 128)) return unsupported(head_dim, heads, kv_heads);
     if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 16) return unsupported(head_dim, heads, kv_heads);
-    if (cap % 32 != 0) return fail(LLMTIE_RAGGED_BLOCK, cap, 32, 0, 0, "a Q8_0 cache capacity of %zu in blocks of 32", cap);
     if (max_tk == 0 || max_tk > cap) return overrun_cache(max_tk, cap);
     if (cap > IMAX || nseq > 65535 || slots > IMAX) return overrun_slice(nseq, 65535);
+    const size_t need = llmtie_q8_cache_bytes(slots, kv_heads, head_dim, cap);
+    if (cache_len < need) return overrun_slice(need, cache_len);
     const size_t n = heads * head_dim;
     if (q_len < nseq * n) return overrun_slice(nseq * n, q_len);
     if (out_len < nseq * n) return overrun_slice(nseq * n, out_len);
     if (nseq == 0) return ok();
-    if (!q || !k_codes || !k_scales || !v_codes || !v_scales || !tk_dev || !slot_dev || !out) return invalid("a buffer");
+    if (!q || !cache || !tk_dev || !slot_dev || !out) return invalid("a buffer");
     if (!scratch) return invalid("scratch");
     const size_t group = heads / kv_heads;
     int nit, splits;
-    plan_decode(max_tk, kv_heads * nseq, nit, splits);
+    plan_decode(max_tk, kv_heads * nseq, group, nit, splits);
     const size_t part = nseq * kv_heads * (size_t)splits * group * (head_dim + 2);
+    const long ml_off = (long)(nseq * kv_heads * (size_t)splits * group * head_dim);
     int r = ensure_scratch(scratch, part, nseq * kv_heads, S(stream));
     if (r != LLMTIE_OK) return r;
     DecodeArgs a;
     memset(&a, 0, sizeof a);
     a.q = q;
-    a.k = k_codes;
-    a.v = v_codes;
-    a.ks = k_scales;
-    a.vs = v_scales;
+    a.k = cache;
     a.out = out;
     a.part = scratch->part;
+    a.ml_off = ml_off;
     a.ctr = scratch->ctr;
     a.tk_arr = tk_dev;
     a.slot_arr = slot_dev;
@@ -401,7 +411,7 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     a.qscale = scale_q ? scale : 1.0f;
     a.nit = nit;
     a.splits = splits;
-    return launched("attn_decode_q8_batch", launch_decode((int)head_dim, KV_Q8, a, (int)kv_heads, (int)nseq, S(stream)));
+    return launched("attn_decode_q8_batch", launch_decode((int)head_dim, KV_TQ8, a, (int)kv_heads, (int)nseq, S(stream)));
 }
 
 int llmtie_rope(void* stream, float* x, size_t x_len, size_t off, const float* freq_div, size_t t, size_t heads,
@@ -488,46 +498,151 @@ int llmtie_cache_grow_f16(void* stream, const uint16_t* src, size_t src_len, uin
     return grow_common(stream, src, src_len, dst, dst_len, 2, kv_heads, head_dim, cap, new_cap, live, transposed);
 }
 
-static int q8_cache_checks(size_t hd, size_t heads, size_t kv, size_t cap, size_t slots, size_t slot) {
+static int q8_cache_checks(size_t hd, size_t heads, size_t kv, size_t cap, size_t slots, size_t slot,
+                           size_t cache_len) {
     if (!(hd == 64 || hd == 128)) return unsupported(hd, heads, kv);
-    if (cap % 32 != 0) return fail(LLMTIE_RAGGED_BLOCK, cap, 32, 0, 0, "a Q8_0 cache capacity of %zu in blocks of 32", cap);
     if (slot >= slots) return overrun_slice(slot + 1, slots);
+    const size_t need = llmtie_q8_cache_bytes(slots, kv, hd, cap);
+    if (cache_len < need) return overrun_slice(need, cache_len);
     return LLMTIE_OK;
 }
 
+size_t llmtie_q8_cache_bytes(size_t slots, size_t kv_heads, size_t head_dim, size_t cap) {
+    return slots * kv_heads * (size_t)tiled_nblk((int)cap) * (size_t)tq8_block_bytes((int)head_dim);
+}
+
+size_t llmtie_t16_cache_len(size_t kv_heads, size_t head_dim, size_t cap) {
+    return kv_heads * (size_t)tiled_nblk((int)cap) * 64 * head_dim;
+}
+
 int llmtie_kv_q8_append(void* stream, const float* k, size_t k_len, size_t k_off, const float* v, size_t v_len,
-                        size_t v_off, int8_t* k_codes, uint16_t* k_scales, int8_t* v_codes, uint16_t* v_scales,
-                        size_t slots, size_t slot, size_t n, size_t kv_heads, size_t head_dim, size_t cap,
-                        size_t past) {
-    int r = q8_cache_checks(head_dim, kv_heads, kv_heads, cap, slots, slot);
+                        size_t v_off, int8_t* cache, size_t cache_len, size_t slots, size_t slot, size_t n,
+                        size_t kv_heads, size_t head_dim, size_t cap, size_t past) {
+    int r = q8_cache_checks(head_dim, kv_heads, kv_heads, cap, slots, slot, cache_len);
     if (r != LLMTIE_OK) return r;
     if (past + n > cap) return overrun_cache(past + n, cap);
     const size_t total = n * kv_heads * head_dim;
     if (k_off + total > k_len) return overrun_slice(k_off + total, k_len);
     if (v_off + total > v_len) return overrun_slice(v_off + total, v_len);
     if (total == 0) return ok();
-    if (!k || !v || !k_codes || !k_scales || !v_codes || !v_scales) return invalid("a buffer");
-    return launched("kv_q8_append", launch_append_q8(k, (long)k_off, v, (long)v_off, k_codes, k_scales, v_codes,
-                                                     v_scales, (int)slot, (int)n, (int)kv_heads, (int)head_dim,
-                                                     (int)cap, (int)past, S(stream)));
+    if (!k || !v || !cache) return invalid("a buffer");
+    return launched("kv_q8_append", launch_append_q8(k, (long)k_off, v, (long)v_off, reinterpret_cast<char*>(cache),
+                                                     (int)slot, (int)n, (int)kv_heads, (int)head_dim, (int)cap,
+                                                     (int)past, S(stream)));
 }
 
 int llmtie_rope_cache_q8(void* stream, float* q, size_t q_len, size_t q_off, const float* k, size_t k_len,
                          size_t k_off, const float* v, size_t v_len, size_t v_off, const float* freq_div,
-                         size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, int8_t* k_codes,
-                         uint16_t* k_scales, int8_t* v_codes, uint16_t* v_scales, size_t slots, size_t slot,
-                         size_t cap) {
-    int r = q8_cache_checks(head_dim, heads, kv_heads, cap, slots, slot);
+                         size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, int8_t* cache,
+                         size_t cache_len, size_t slots, size_t slot, size_t cap) {
+    int r = q8_cache_checks(head_dim, heads, kv_heads, cap, slots, slot, cache_len);
     if (r != LLMTIE_OK) return r;
     if (pos >= cap) return overrun_cache(pos + 1, cap);
     if (q_off + heads * head_dim > q_len) return overrun_slice(q_off + heads * head_dim, q_len);
     if (k_off + kv_heads * head_dim > k_len) return overrun_slice(k_off + kv_heads * head_dim, k_len);
     if (v_off + kv_heads * head_dim > v_len) return overrun_slice(v_off + kv_heads * head_dim, v_len);
-    if (!q || !k || !v || !k_codes || !k_scales || !v_codes || !v_scales) return invalid("a buffer");
+    if (!q || !k || !v || !cache) return invalid("a buffer");
     return launched("rope_cache_q8", launch_rope_cache_q8(q, (long)q_off, k, (long)k_off, v, (long)v_off, freq_div,
                                                           (int)heads, (int)kv_heads, (int)head_dim, theta, (int)pos,
-                                                          k_codes, k_scales, v_codes, v_scales, (int)slot, (int)cap,
+                                                          reinterpret_cast<char*>(cache), (int)slot, (int)cap,
                                                           S(stream)));
+}
+
+// ------------------------------------------------------------ tiled f16
+
+static int t16_checks(size_t hd, size_t heads, size_t kv, size_t cap, size_t cache_len) {
+    if (!(hd == 64 || hd == 128) || kv == 0) return unsupported(hd, heads, kv);
+    if (cap > IMAX) return overrun_slice(cap, IMAX);
+    const size_t need = llmtie_t16_cache_len(kv, hd, cap);
+    if (cache_len < need) return overrun_slice(need, cache_len);
+    return LLMTIE_OK;
+}
+
+int llmtie_t16_append(void* stream, const float* src, size_t src_len, size_t src_off, uint16_t* cache,
+                      size_t cache_len, size_t n, size_t kv_heads, size_t head_dim, size_t cap, size_t past,
+                      int value) {
+    int r = t16_checks(head_dim, kv_heads, kv_heads, cap, cache_len);
+    if (r != LLMTIE_OK) return r;
+    if (past + n > cap) return overrun_cache(past + n, cap);
+    const size_t total = n * kv_heads * head_dim;
+    if (src_off + total > src_len) return overrun_slice(src_off + total, src_len);
+    if (total == 0) return ok();
+    if (!src || !cache) return invalid("a buffer");
+    return launched("t16_append", launch_append_t16(src, (long)src_off, cache, (int)n, (int)kv_heads, (int)head_dim,
+                                                    (int)cap, (int)past, value ? 1 : 0, S(stream)));
+}
+
+int llmtie_t16_rope_cache(void* stream, float* q, size_t q_len, size_t q_off, const float* k, size_t k_len,
+                          size_t k_off, const float* v, size_t v_len, size_t v_off, const float* freq_div,
+                          size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, uint16_t* cache,
+                          size_t cache_len, size_t cap) {
+    int r = t16_checks(head_dim, heads, kv_heads, cap, cache_len);
+    if (r != LLMTIE_OK) return r;
+    if (pos >= cap) return overrun_cache(pos + 1, cap);
+    if (q_off + heads * head_dim > q_len) return overrun_slice(q_off + heads * head_dim, q_len);
+    if (k_off + kv_heads * head_dim > k_len) return overrun_slice(k_off + kv_heads * head_dim, k_len);
+    if (v_off + kv_heads * head_dim > v_len) return overrun_slice(v_off + kv_heads * head_dim, v_len);
+    if (!q || !k || !v || !cache) return invalid("a buffer");
+    return launched("t16_rope_cache",
+                    launch_rope_cache_t16(q, (long)q_off, k, (long)k_off, v, (long)v_off, freq_div, (int)heads,
+                                          (int)kv_heads, (int)head_dim, theta, (int)pos, cache, (int)cap, S(stream)));
+}
+
+int llmtie_t16_grow(void* stream, const uint16_t* src, size_t src_len, uint16_t* dst, size_t dst_len,
+                    size_t kv_heads, size_t head_dim, size_t cap, size_t new_cap, size_t live) {
+    if (live > cap || new_cap < cap) return overrun_cache(std::max(live, cap), std::min(new_cap, cap));
+    int r = t16_checks(head_dim, kv_heads, kv_heads, cap, src_len);
+    if (r != LLMTIE_OK) return r;
+    r = t16_checks(head_dim, kv_heads, kv_heads, new_cap, dst_len);
+    if (r != LLMTIE_OK) return r;
+    const size_t bl = 64 * head_dim;  // halves per block
+    const size_t rows = kv_heads, len = (size_t)tiled_nblk((int)live) * bl;
+    if (rows * len == 0) return ok();
+    if (!src || !dst) return invalid("a buffer");
+    return launched("t16_grow", launch_grow(src, dst, 2, (int)rows, (int)len, (int)(tiled_nblk((int)cap) * bl),
+                                            (int)(tiled_nblk((int)new_cap) * bl), S(stream)));
+}
+
+int llmtie_t16_from_ref(void* stream, const uint16_t* k, size_t k_len, const uint16_t* v, size_t v_len,
+                        size_t kv_heads, size_t head_dim, size_t cap, size_t live, uint16_t* cache,
+                        size_t cache_len) {
+    int r = t16_checks(head_dim, kv_heads, kv_heads, cap, cache_len);
+    if (r != LLMTIE_OK) return r;
+    if (live > cap) return overrun_cache(live, cap);
+    const size_t need = kv_heads * cap * head_dim;
+    if (k_len < need || v_len < need) return overrun_slice(need, std::min(k_len, v_len));
+    if (live == 0) return ok();
+    if (!k || !v || !cache) return invalid("a buffer");
+    return launched("t16_from_ref", launch_ref_to_t16(k, v, cache, (int)kv_heads, (int)head_dim, (int)cap, (int)live,
+                                                      (int)cap, S(stream)));
+}
+
+int llmtie_attn_decode_t16(void* stream, const float* q, size_t q_len, const uint16_t* cache, size_t cache_len,
+                           size_t heads, size_t kv_heads, size_t head_dim, size_t tk, size_t cap, float scale,
+                           int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len) {
+    return decode_common(stream, KV_T16, q, q_len, 0, cache, cache_len, nullptr, 0, heads, kv_heads, head_dim, tk,
+                         cap, scale, scale_q, scratch, out, out_len, 0, nullptr, 0, 0, false);
+}
+
+int llmtie_attn_decode_t16_q_row(void* stream, const float* q, size_t q_len, size_t q_off, const uint16_t* cache,
+                                 size_t cache_len, size_t heads, size_t kv_heads, size_t head_dim, size_t tk,
+                                 size_t cap, float scale, int scale_q, llmtie_decode_scratch* scratch, float* out,
+                                 size_t out_len, int8_t* twin, size_t twin_rows, size_t twin_k, size_t row) {
+    return decode_common(stream, KV_T16, q, q_len, q_off, cache, cache_len, nullptr, 0, heads, kv_heads, head_dim,
+                         tk, cap, scale, scale_q, scratch, out, out_len, row * heads * head_dim, twin, twin_rows,
+                         twin_k, twin != nullptr);
+}
+
+int llmtie_flash_attn_t16(void* stream, const float* q, size_t q_len, const uint16_t* cache, size_t cache_len,
+                          float* out, size_t out_len, size_t tq, size_t past, size_t heads, size_t kv_heads,
+                          size_t head_dim, size_t cap, float scale, int causal) {
+    int r = t16_checks(head_dim, heads, kv_heads, cap, cache_len);
+    if (r != LLMTIE_OK) return r;
+    // The tiled cache holds both areas in one buffer; the length checks of the
+    // shared path are satisfied by passing the whole-cache extent for both.
+    const size_t ext = kv_heads * cap * head_dim;
+    return prefill_common(stream, PF_T16, q, q_len, cache, ext, cache, ext, out, out_len, tq, past, heads, kv_heads,
+                          head_dim, cap, scale, causal);
 }
 
 }  // extern "C"

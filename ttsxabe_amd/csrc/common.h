@@ -101,3 +101,15 @@ __device__ __forceinline__ float sum4grp(float v) {
     v += __shfl_xor(v, 32, 64);
     return v;
 }
+
+// Agent-scope (device-coherent) 32-bit store and loads: visible across the
+// XCDs' separate L2s without a cache-wide fence.
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4 ld_coherent4(const float* p) {
+    return make_float4(ld_coherent(p), ld_coherent(p + 1), ld_coherent(p + 2), ld_coherent(p + 3));
+}

@@ -5,22 +5,22 @@
 
 namespace llmtie {
 
-enum KvKind { KV_F16 = 0, KV_F32 = 1, KV_Q8 = 2 };
+enum KvKind { KV_F16 = 0, KV_F32 = 1, KV_T16 = 2, KV_TQ8 = 3 };
 
-// Upper bound on splits per head: the merging workgroup keeps one weight per
-// split and query head in LDS.
+// Upper bounds on splits per head: the merging workgroup keeps (m, l) per
+// split and query head in LDS, at most DECODE_MAX_SPLIT_ROWS of them.
 constexpr int DECODE_MAX_SPLITS = 256;
+constexpr int DECODE_MAX_SPLIT_ROWS = 1024;
 
 struct DecodeArgs {
     const float* q;          // query rows, f32
-    const void* k;           // K values or codes
-    const void* v;           // V^T values or codes
-    const uint16_t* ks;      // Q8_0 scales of K (f16 bits), else null
-    const uint16_t* vs;      // Q8_0 scales of V (f16 bits), else null
+    const void* k;           // K values (reference layouts) or the tiled block array
+    const void* v;           // V^T values (reference layouts); unused for tiled layouts
     float* out;              // context rows, f32
     int8_t* twin_codes;      // int8 twin of the context, or null
     float* twin_scales;      // its per-32 scales
-    float* part;             // split partials
+    float* part;             // split partials: O area, then the (m, l) area at ml_off
+    long ml_off;             // floats from part to the (m, l) area
     unsigned* ctr;           // one arrival counter per (sequence, kv head), zero between calls
     const int* tk_arr;       // per-sequence live lengths (batched) or null
     const int* slot_arr;     // per-sequence cache slot (batched) or null
@@ -28,7 +28,7 @@ struct DecodeArgs {
     long out_off, out_stride;
     int tk;                  // live length, or the bound every tk_arr entry is clamped to
     int slots;               // cache slots (batched)
-    int cap;                 // positions per cache row
+    int cap;                 // positions per cache row (tiled: rounded up to whole blocks)
     int kv_heads;            // kv heads per slot
     int group;               // query heads per kv head (<= 16)
     float score_l2;          // raw dot product -> log2-unit score

@@ -5,9 +5,12 @@
 // MFMA kernel, templated on the head width and on the cache's storage:
 //   KV_F16 - K [kv][cap][hd] f16, V [kv][hd][cap] f16 (the reference layout)
 //   KV_F32 - the same layout at f32 (the Whisper decoder's self cache)
-//   KV_Q8  - GGUF Q8_0 blocks (32 int8 codes + one f16 scale per 32 dims of a
-//            position): K codes [slot][kv][cap][hd], V codes transposed
-//            [slot][kv][hd][cap], scales of both [slot][kv][cap][hd/32].
+//   KV_T16 - the tiled f16 layout of kvlayout.h (fragment order)
+//   KV_TQ8 - the tiled GGUF Q8_0 layout of kvlayout.h (32 int8 codes + one f16
+//            scale per 32 dims of a position), for batched sequences in slots.
+// The tiled layouts make every K/V load a contiguous 1 KB wave-wide read; off
+// the reference layout a load instruction touches 16 rows, which measured at
+// about half the achievable HBM rate for the same bytes.
 //
 // Work decomposition. A workgroup is four waves on one (sequence, kv head,
 // split); a split is `4 * nit` blocks of 32 consecutive keys and wave w takes
@@ -36,11 +39,33 @@
 // which workgroup finishes last, so repeated calls are bit-identical.
 #include "common.h"
 #include "decode.h"
+#include "kvlayout.h"
 
 namespace llmtie {
 
-constexpr int DW = 4;              // waves per workgroup
+constexpr int DW = 4;                 // waves per workgroup
 constexpr int DT = DW * LLMTIE_WAVE;  // threads per workgroup
+
+// Eight int8 codes (two dwords) as eight exact halves: flip the sign bit to
+// get c + 128, splice each byte under the exponent byte 0x64 (the half
+// 1024 + (c + 128)), and subtract 1152 with one packed f16 add per pair.
+__device__ __forceinline__ half8 dq8(uint32_t w0, uint32_t w1) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
+    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)};
+    const h2 bias = {(half_t)1152.0f, (half_t)1152.0f};
+    half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const h2 v = __builtin_bit_cast(h2, p[i]) - bias;
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
 
 template <int HD, int KIND>
 struct Frag;
@@ -51,155 +76,184 @@ struct Frag<HD, KV_F16> {
     half8 v[HD / 16];
 };
 template <int HD>
+struct Frag<HD, KV_T16> {
+    half8 k[2][HD / 32];
+    half8 v[HD / 16];
+};
+template <int HD>
 struct Frag<HD, KV_F32> {
     half8 kh[2][HD / 32], kl[2][HD / 32];
     half8 vh[HD / 16], vl[HD / 16];
 };
+// Raw codes and scales, dequantised where they are used.
 template <int HD>
-struct Frag<HD, KV_Q8> {
-    half8 k[2][HD / 32];
-    half8 v[HD / 16];
-    half_t dk[8][HD / 32];  // scales of keys 8*grp + j, block b
-    half_t dv[8][HD / 32];
+struct Frag<HD, KV_TQ8> {
+    uint4 kc[2][HD / 64];  // (T, step pair)
+    uint4 vc[HD / 32];     // tile pair
+    uint4 ks[HD / 32];     // keys 8g .. 8g+7 x all dim blocks, key-major
+    uint4 vs[HD / 32];
 };
 
 struct Ctx {
-    const char* k;   // this (sequence, kv head)'s K base (codes or values)
-    const char* v;   // V^T base
-    const uint16_t* ks;  // Q8 scales of K, row of key 0
-    const uint16_t* vs;
+    const char* k;   // reference layouts: K base of this kv head; tiled: block 0 of this (slot, kv head)
+    const char* v;   // reference layouts: V^T base of this kv head
+    long bstride;    // tiled: bytes per block
     int tk, cap;
-    bool v16;  // V rows are 16-byte aligned at every 8-key boundary
 };
 
-template <int HD, int KIND>
-__device__ __forceinline__ void load_block(const Ctx& c, int p0, int col, int grp, Frag<HD, KIND>& f) {
-    constexpr int NS = HD / 32;
-    constexpr int NT = HD / 16;
-    // Keys.
+// Eight consecutive V^T elements (one value row, keys kb..kb+7) off the
+// reference layout as f16 hi/lo or exact f16. VA is the alignment the row
+// start guarantees (16 or 8 bytes).
+template <int KIND, int VA>
+__device__ __forceinline__ void v_row8(const Ctx& c, size_t row, half8& h, half8& l) {
+    if constexpr (KIND == KV_F16) {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(c.v) + row;
+        if constexpr (VA == 16) {
+            h = ld_h8(p);
+        } else {
+            const uint2 a = reinterpret_cast<const uint2*>(p)[0];
+            const uint2 b = reinterpret_cast<const uint2*>(p)[1];
+            const uint32_t w[4] = {a.x, a.y, b.x, b.y};
 #pragma unroll
-    for (int T = 0; T < 2; ++T) {
-        const int key = p0 + 8 * (col >> 2) + 4 * T + (col & 3);
-        const bool ok = key < c.tk;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int d0 = 32 * s + 8 * grp;
-            if constexpr (KIND == KV_F16) {
-                f.k[T][s] = ok ? ld_h8(c.k + ((size_t)key * HD + d0) * 2) : zero_h8();
-            } else if constexpr (KIND == KV_F32) {
-                half8 h = zero_h8(), l = zero_h8();
-                if (ok) {
-                    const float4* p = reinterpret_cast<const float4*>(c.k + ((size_t)key * HD + d0) * 4);
-                    const float4 a = p[0], b = p[1];
-                    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        half_t hh, ll;
-                        split_h(x[j], hh, ll);
-                        h[j] = hh;
-                        l[j] = ll;
-                    }
-                }
-                f.kh[T][s] = h;
-                f.kl[T][s] = l;
-            } else {
-                f.k[T][s] = ok ? ld_q8x8(reinterpret_cast<const int8_t*>(c.k) + (size_t)key * HD + d0) : zero_h8();
+            for (int i = 0; i < 4; ++i) {
+                h[2 * i] = __builtin_bit_cast(half_t, (uint16_t)(w[i] & 0xffffu));
+                h[2 * i + 1] = __builtin_bit_cast(half_t, (uint16_t)(w[i] >> 16));
             }
         }
-    }
-    // Values: V^T rows d = 16t + col, keys p0 + 8*grp + 0..7.
-    const int kb = p0 + 8 * grp;
-    const bool full = kb + 8 <= c.tk;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const size_t row = (size_t)(16 * t + col) * c.cap + kb;
-        if constexpr (KIND == KV_F16) {
-            const uint16_t* p = reinterpret_cast<const uint16_t*>(c.v) + row;
-            if (full) {
-                f.v[t] = c.v16 ? ld_h8(p) : ld_h8_a4(p);
-            } else {
-                half8 h = zero_h8();
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (kb + j < c.tk) h[j] = __builtin_bit_cast(half_t, p[j]);
-                f.v[t] = h;
-            }
-        } else if constexpr (KIND == KV_F32) {
-            const float* p = reinterpret_cast<const float*>(c.v) + row;
-            float x[8];
-            if (full) {
-                if (c.v16) {
-                    const float4 a = reinterpret_cast<const float4*>(p)[0];
-                    const float4 b = reinterpret_cast<const float4*>(p)[1];
-                    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-                    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        const float2 a = reinterpret_cast<const float2*>(p + j)[0];
-                        x[j] = a.x;
-                        x[j + 1] = a.y;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = (kb + j < c.tk) ? p[j] : 0.0f;
-            }
-            half8 h, l;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                half_t hh, ll;
-                split_h(x[j], hh, ll);
-                h[j] = hh;
-                l[j] = ll;
-            }
-            f.vh[t] = h;
-            f.vl[t] = l;
+    } else {
+        const float* p = reinterpret_cast<const float*>(c.v) + row;
+        float x[8];
+        if constexpr (VA == 16) {
+            const float4 a = reinterpret_cast<const float4*>(p)[0];
+            const float4 b = reinterpret_cast<const float4*>(p)[1];
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+            x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
         } else {
-            const int8_t* p = reinterpret_cast<const int8_t*>(c.v) + row;
-            if (full) {
-                f.v[t] = ld_q8x8(p);
-            } else {
-                half8 h = zero_h8();
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (kb + j < c.tk) h[j] = (half_t)(float)p[j];
-                f.v[t] = h;
+            for (int j = 0; j < 8; j += 2) {
+                const float2 a = reinterpret_cast<const float2*>(p + j)[0];
+                x[j] = a.x;
+                x[j + 1] = a.y;
             }
         }
-    }
-    if constexpr (KIND == KV_Q8) {
-        // Scales of keys kb .. kb + 7, every block: 8 * HD/32 contiguous halves.
-        constexpr int NB = HD / 32;
-        const uint16_t* ks = c.ks + (size_t)kb * NB;
-        const uint16_t* vs = c.vs + (size_t)kb * NB;
-        if (full) {
 #pragma unroll
-            for (int i = 0; i < NB; ++i) {
-                // 16 bytes = 8 halves = keys 2i, 2i+1 (NB == 4) or 4i..4i+3 (NB == 2)
-                const half8 a = ld_h8(ks + 8 * i);
-                const half8 b = ld_h8(vs + 8 * i);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    f.dk[(8 * i + e) / NB][(8 * i + e) % NB] = a[e];
-                    f.dv[(8 * i + e) / NB][(8 * i + e) % NB] = b[e];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const bool ok = kb + j < c.tk;
-                    f.dk[j][b] = ok ? __builtin_bit_cast(half_t, ks[j * NB + b]) : (half_t)0.0f;
-                    f.dv[j][b] = ok ? __builtin_bit_cast(half_t, vs[j * NB + b]) : (half_t)0.0f;
-                }
+        for (int j = 0; j < 8; ++j) {
+            half_t hh, ll;
+            split_h(x[j], hh, ll);
+            h[j] = hh;
+            l[j] = ll;
         }
     }
 }
 
-// One 32-key block folded into the wave's running softmax state.
-template <int HD, int KIND>
+// Loads the 32-key block starting at p0 (block index p0 / 32).
+// Tiled layouts: straight 16-byte-per-lane reads, always in bounds (a tiled
+// cache holds whole blocks); keys >= tk are dropped later by the fold.
+// Reference layouts: FULL = every key of the block is live, so nothing is
+// guarded; !FULL = the one partial block at the end of the context, where
+// keys >= tk read as zero and nothing past tk is touched.
+template <int HD, int KIND, int VA, bool FULL>
+__device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<HD, KIND>& f) {
+    constexpr int NS = HD / 32;
+    constexpr int NT = HD / 16;
+    const int col = lane & 15, grp = lane >> 4;
+    if constexpr (KIND == KV_T16) {
+        const half8* b = reinterpret_cast<const half8*>(c.k + (long)(p0 >> 5) * c.bstride);
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int s = 0; s < NS; ++s) f.k[T][s] = b[(T * NS + s) * 64 + lane];
+        const half8* vb = b + 4 * HD;  // the V area: 32*HD halves in
+#pragma unroll
+        for (int t = 0; t < NT; ++t) f.v[t] = vb[t * 64 + lane];
+    } else if constexpr (KIND == KV_TQ8) {
+        const char* b = c.k + (long)(p0 >> 5) * c.bstride;
+        const uint4* kc = reinterpret_cast<const uint4*>(b);
+        const uint4* vc = reinterpret_cast<const uint4*>(b + 32 * HD);
+        const uint4* ks = reinterpret_cast<const uint4*>(b + 64 * HD);
+        const uint4* vs = reinterpret_cast<const uint4*>(b + 64 * HD + 64 * (HD / 32));
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int sp = 0; sp < NS / 2; ++sp) f.kc[T][sp] = kc[(T * (NS / 2) + sp) * 64 + lane];
+#pragma unroll
+        for (int tp = 0; tp < NT / 2; ++tp) f.vc[tp] = vc[tp * 64 + lane];
+        // Keys 8*grp .. +7, all NS dim blocks: NS 16-byte pieces per lane.
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            f.ks[i] = ks[grp * NS + i];
+            f.vs[i] = vs[grp * NS + i];
+        }
+    } else {
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+            const int key = p0 + 8 * (col >> 2) + 4 * T + (col & 3);
+            const bool ok = FULL || key < c.tk;
+            const int kk = ok ? key : 0;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int d0 = 32 * s + 8 * grp;
+                if constexpr (KIND == KV_F16) {
+                    const half8 x = ld_h8(c.k + ((size_t)kk * HD + d0) * 2);
+                    f.k[T][s] = ok ? x : zero_h8();
+                } else {
+                    const float4* p = reinterpret_cast<const float4*>(c.k + ((size_t)kk * HD + d0) * 4);
+                    const float4 a = p[0], b = p[1];
+                    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                    half8 h, l;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        half_t hh, ll;
+                        split_h(ok ? x[j] : 0.0f, hh, ll);
+                        h[j] = hh;
+                        l[j] = ll;
+                    }
+                    f.kh[T][s] = h;
+                    f.kl[T][s] = l;
+                }
+            }
+        }
+        const int kb = p0 + 8 * grp;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const size_t row = (size_t)(16 * t + col) * c.cap + kb;
+            half8 h = zero_h8(), l = zero_h8();
+            if constexpr (FULL) {
+                v_row8<KIND, VA>(c, row, h, l);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (kb + j < c.tk) {
+                        if constexpr (KIND == KV_F16) {
+                            h[j] = __builtin_bit_cast(half_t, reinterpret_cast<const uint16_t*>(c.v)[row + j]);
+                        } else {
+                            half_t hh, ll;
+                            split_h(reinterpret_cast<const float*>(c.v)[row + j], hh, ll);
+                            h[j] = hh;
+                            l[j] = ll;
+                        }
+                    }
+                }
+            }
+            if constexpr (KIND == KV_F32) {
+                f.vh[t] = h;
+                f.vl[t] = l;
+            } else {
+                f.v[t] = h;
+            }
+        }
+    }
+}
+
+// Half j of a 16-byte piece (keys 8g+j .. for scales: element e).
+__device__ __forceinline__ half_t h_at(const uint4& u, int e) {
+    const uint32_t w = e < 2 ? u.x : e < 4 ? u.y : e < 6 ? u.z : u.w;
+    return __builtin_bit_cast(half_t, (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+
+// One 32-key block folded into the wave's running softmax state. MASK: keys
+// >= tk are dropped (only the partial block needs it).
+template <int HD, int KIND, bool MASK>
 __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 (&qh)[HD / 32],
                                            const half8 (&ql)[HD / 32], int p0, int tk, int grp,
                                            float score_l2, float& m_run, float& l_run,
@@ -212,7 +266,7 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
         floatx4 acc = zero_f4();
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            if constexpr (KIND == KV_F16) {
+            if constexpr (KIND == KV_F16 || KIND == KV_T16) {
                 acc = mfma16(f.k[T][s], qh[s], acc);
                 acc = mfma16(f.k[T][s], ql[s], acc);
             } else if constexpr (KIND == KV_F32) {
@@ -220,10 +274,16 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
                 acc = mfma16(f.kh[T][s], ql[s], acc);
                 acc = mfma16(f.kl[T][s], qh[s], acc);
             } else {
-                floatx4 b = mfma16(f.k[T][s], qh[s], zero_f4());
-                b = mfma16(f.k[T][s], ql[s], b);
+                const uint4& w = f.kc[T][s >> 1];
+                const half8 kq = (s & 1) ? dq8(w.z, w.w) : dq8(w.x, w.y);
+                floatx4 b = mfma16(kq, qh[s], zero_f4());
+                b = mfma16(kq, ql[s], b);
+                // Key 8g + 4T + r, dim block s: element (4T + r) * NS + s of the scale run.
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[r] += (float)f.dk[4 * T + r][s] * b[r];
+                for (int r = 0; r < 4; ++r) {
+                    const int e = (4 * T + r) * NS + s;
+                    acc[r] += (float)h_at(f.ks[e >> 3], e & 7) * b[r];
+                }
             }
         }
 #pragma unroll
@@ -233,7 +293,7 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
     float mx = ninf();
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        sc[j] = (kb + j < tk) ? sc[j] * score_l2 : ninf();
+        sc[j] = (!MASK || kb + j < tk) ? sc[j] * score_l2 : ninf();
         mx = fmaxf(mx, sc[j]);
     }
     mx = max4grp(mx);
@@ -250,22 +310,24 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
 #pragma unroll
     for (int t = 0; t < NT; ++t) o[t] *= fac;
 
-    if constexpr (KIND == KV_Q8) {
-        constexpr int NB = HD / 32;
+    if constexpr (KIND == KV_TQ8) {
+        // P' = P * d_v (the scale of each key's dim block) as one f16 operand
+        // per block: Q8_0 values carry 8 bits, so the 11 of an f16 P' keep
+        // the product well inside the quantisation's own error.
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            half8 ph, pl;
+        for (int b = 0; b < NS; ++b) {
+            half8 pv;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                half_t hh, ll;
-                split_h(p[j] * (float)f.dv[j][b], hh, ll);
-                ph[j] = hh;
-                pl[j] = ll;
+                const int e = j * NS + b;
+                const float d = (float)h_at(f.vs[e >> 3], e & 7);
+                pv[j] = to_h((!MASK || kb + j < tk) ? p[j] * d : 0.0f);
             }
 #pragma unroll
             for (int t = 2 * b; t < 2 * b + 2; ++t) {
-                o[t] = mfma16(f.v[t], ph, o[t]);
-                o[t] = mfma16(f.v[t], pl, o[t]);
+                const uint4& w = f.vc[t >> 1];
+                const half8 vq = (t & 1) ? dq8(w.z, w.w) : dq8(w.x, w.y);
+                o[t] = mfma16(vq, pv, o[t]);
             }
         }
     } else {
@@ -282,6 +344,16 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
             if constexpr (KIND == KV_F16) {
                 o[t] = mfma16(f.v[t], ph, o[t]);
                 o[t] = mfma16(f.v[t], pl, o[t]);
+            } else if constexpr (KIND == KV_T16) {
+                // A tiled cache holds garbage past tk: zero those keys' values so
+                // that 0 * (a non-finite half) cannot reach the sum.
+                half8 vv = f.v[t];
+                if constexpr (MASK) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) vv[j] = (kb + j < tk) ? vv[j] : (half_t)0.0f;
+                }
+                o[t] = mfma16(vv, ph, o[t]);
+                o[t] = mfma16(vv, pl, o[t]);
             } else {
                 o[t] = mfma16(f.vh[t], ph, o[t]);
                 o[t] = mfma16(f.vh[t], pl, o[t]);
@@ -306,12 +378,13 @@ __device__ __forceinline__ void emit(float* out, int8_t* tc, float* ts, size_t i
     }
 }
 
-template <int HD, int KIND>
-__global__ __launch_bounds__(DT) void attn_decode_kernel(DecodeArgs a) {
+template <int HD, int KIND, int VA>
+__global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel(DecodeArgs a) {
     constexpr int NS = HD / 32;
     constexpr int NT = HD / 16;
+    constexpr bool TILED = KIND == KV_T16 || KIND == KV_TQ8;
     constexpr int OBS = HD * 17;  // one wave's O^T in LDS, padded
-    __shared__ float lds[DW * OBS > 16 * DECODE_MAX_SPLITS ? DW * OBS : 16 * DECODE_MAX_SPLITS];
+    __shared__ float lds[DW * OBS];
     __shared__ float wm[DW][16], wl[DW][16], gm[16], gl[16];
     __shared__ int last;
 
@@ -338,33 +411,51 @@ __global__ __launch_bounds__(DT) void attn_decode_kernel(DecodeArgs a) {
     c.tk = tk;
     c.cap = a.cap;
     const size_t kvh = (size_t)slot * a.kv_heads + h;
-    const int esz = KIND == KV_F32 ? 4 : (KIND == KV_F16 ? 2 : 1);
-    c.k = reinterpret_cast<const char*>(a.k) + kvh * a.cap * HD * esz;
-    c.v = reinterpret_cast<const char*>(a.v) + kvh * HD * a.cap * esz;
-    c.ks = a.ks ? a.ks + kvh * a.cap * (HD / 32) : nullptr;
-    c.vs = a.vs ? a.vs + kvh * a.cap * (HD / 32) : nullptr;
-    c.v16 = ((a.cap * esz) & 15) == 0;
+    if constexpr (TILED) {
+        c.bstride = KIND == KV_T16 ? 2L * 32 * HD * 2 : tq8_block_bytes(HD);
+        c.k = reinterpret_cast<const char*>(a.k) + kvh * (size_t)tiled_nblk(a.cap) * c.bstride;
+        c.v = nullptr;
+    } else {
+        constexpr int esz = KIND == KV_F32 ? 4 : 2;
+        c.bstride = 0;
+        c.k = reinterpret_cast<const char*>(a.k) + kvh * a.cap * HD * esz;
+        c.v = reinterpret_cast<const char*>(a.v) + kvh * HD * a.cap * esz;
+    }
 
-    // The group's queries as B operands, hi + lo.
+    // This wave's blocks: b_i = first + i * DW for i < nit; full blocks first,
+    // through a two-deep pipeline (block i+1's loads in flight while block i
+    // is folded), then the context's one partial block if it is this wave's.
+    // The first block's loads go out before the queries are read.
+    const int first = split * DW * a.nit + wave;
+    const int nfull = tk >> 5;
+    const int nf = nfull > first ? min(a.nit, (nfull - first + DW - 1) / DW) : 0;
+    const bool tail = (tk & 31) && nfull >= first && (nfull - first) % DW == 0 && (nfull - first) / DW < a.nit;
+    Frag<HD, KIND> f0, f1;
+    if (nf > 0) load_block<HD, KIND, VA, true>(c, first * 32, lane, f0);
+
+    // The group's queries as B operands, hi + lo (columns past the group are
+    // read from column 0 and zeroed, so every load is unconditional).
     const float* q = a.q + a.q_off + (size_t)seq * a.q_stride + ((size_t)h * group) * HD;
+    const bool qok = col < group;
+    const float* qc = q + (size_t)(qok ? col : 0) * HD + 8 * grp;
+    float4 qx[NS][2];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        qx[s][0] = reinterpret_cast<const float4*>(qc + 32 * s)[0];
+        qx[s][1] = reinterpret_cast<const float4*>(qc + 32 * s)[1];
+    }
     half8 qh[NS], ql[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        half8 hv = zero_h8(), lv = zero_h8();
-        if (col < group) {
-            const float4* p = reinterpret_cast<const float4*>(q + (size_t)col * HD + 32 * s + 8 * grp);
-            const float4 x0 = p[0], x1 = p[1];
-            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float x[8] = {qx[s][0].x, qx[s][0].y, qx[s][0].z, qx[s][0].w,
+                            qx[s][1].x, qx[s][1].y, qx[s][1].z, qx[s][1].w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                half_t hh, ll;
-                split_h(x[j] * a.qscale, hh, ll);
-                hv[j] = hh;
-                lv[j] = ll;
-            }
+        for (int j = 0; j < 8; ++j) {
+            half_t hh, ll;
+            split_h(qok ? x[j] * a.qscale : 0.0f, hh, ll);
+            qh[s][j] = hh;
+            ql[s][j] = ll;
         }
-        qh[s] = hv;
-        ql[s] = lv;
     }
 
     float m_run = ninf(), l_run = 0.0f;
@@ -372,21 +463,19 @@ __global__ __launch_bounds__(DT) void attn_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) o[t] = zero_f4();
 
-    // Blocks of this wave: p(i) = split*span + (i*DW + wave)*32, i < nit.
-    const int base = split * span + wave * 32;
-    Frag<HD, KIND> f0, f1;
-    if (base < tk) load_block<HD, KIND>(c, base, col, grp, f0);
-    for (int i = 0; i < a.nit; i += 2) {
-        const int p0 = base + i * DW * 32;
+    int i = 0;
+    for (; i + 1 < nf; i += 2) {
+        const int p0 = (first + i * DW) * 32;
         const int p1 = p0 + DW * 32;
-        const int p2 = p1 + DW * 32;
-        if (p0 >= tk) break;
-        const bool has1 = i + 1 < a.nit && p1 < tk;
-        const bool has2 = i + 2 < a.nit && p2 < tk;
-        if (has1) load_block<HD, KIND>(c, p1, col, grp, f1);
-        fold_block<HD, KIND>(f0, qh, ql, p0, tk, grp, a.score_l2, m_run, l_run, o);
-        if (has2) load_block<HD, KIND>(c, p2, col, grp, f0);
-        if (has1) fold_block<HD, KIND>(f1, qh, ql, p1, tk, grp, a.score_l2, m_run, l_run, o);
+        load_block<HD, KIND, VA, true>(c, p1, lane, f1);
+        fold_block<HD, KIND, false>(f0, qh, ql, p0, tk, grp, a.score_l2, m_run, l_run, o);
+        if (i + 2 < nf) load_block<HD, KIND, VA, true>(c, p1 + DW * 32, lane, f0);
+        fold_block<HD, KIND, false>(f1, qh, ql, p1, tk, grp, a.score_l2, m_run, l_run, o);
+    }
+    if (i < nf) fold_block<HD, KIND, false>(f0, qh, ql, (first + i * DW) * 32, tk, grp, a.score_l2, m_run, l_run, o);
+    if (tail) {
+        load_block<HD, KIND, VA, TILED>(c, nfull * 32, lane, f0);
+        fold_block<HD, KIND, true>(f0, qh, ql, nfull * 32, tk, grp, a.score_l2, m_run, l_run, o);
     }
     l_run = sum4grp(l_run);
 
@@ -437,82 +526,115 @@ __global__ __launch_bounds__(DT) void attn_decode_kernel(DecodeArgs a) {
         return;
     }
 
-    // Publish this split's partial: [g][HD] O (relative to its own max), m, l.
-    const size_t rec = (size_t)(HD + 2);
-    const size_t head_part = (((size_t)seq * gridDim.y + h) * a.splits) * group * rec;
-    float* mine = a.part + head_part + (size_t)split * group * rec;
+    // Publish this split's partial: O [g][HD] (relative to its own max) in
+    // the O area, (m, l) per g in the ML area.
+    const size_t head = (size_t)seq * gridDim.y + h;
+    float* po = a.part + (head * a.splits) * n;
+    float* pml = a.part + a.ml_off + (head * a.splits) * group * 2;
+    // Cross-workgroup hand-off without cache-wide fences: the partial is
+    // stored with agent-scope (coherent) stores, the stores are waited for,
+    // and only then is the arrival counted; the last arriver reads the
+    // partials with agent-scope loads. A release/acquire fence pair would
+    // write back and invalidate the whole L2 of the XCD on every workgroup,
+    // which measured several times the cost of the attention itself.
     for (int e = tid; e < n; e += DT) {
         const int g = e / HD, d = e % HD;
         float acc = 0.0f;
 #pragma unroll
         for (int w = 0; w < DW; ++w) acc += lds[w * OBS + d * 17 + g];
-        mine[g * rec + d] = acc;
+        st_coherent(po + (size_t)split * n + e, acc);
     }
     if (tid < group) {
-        mine[tid * rec + HD] = gm[tid];
-        mine[tid * rec + HD + 1] = gl[tid];
+        st_coherent(pml + ((size_t)split * group + tid) * 2, gm[tid]);
+        st_coherent(pml + ((size_t)split * group + tid) * 2 + 1, gl[tid]);
     }
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    unsigned* ctr = a.ctr + (size_t)seq * gridDim.y + h;
+    unsigned* ctr = a.ctr + head;
     if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = prev == (unsigned)(nsplit - 1);
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
-    // The merge, in split order. Per group: a wave finds the max and the
-    // weights 2^(m_s - M) (kept in LDS), and the sum L.
-    const float* all = a.part + head_part;
-    float* wts = lds;  // [16][DECODE_MAX_SPLITS]
-    __syncthreads();   // everyone is done reading `lds` as O^T
-    for (int g = wave; g < group; g += DW) {
+    // The merge, in split order, with every load of it issued before any is
+    // waited on: one memory round trip. Thread t owns float4 column
+    // c = t % C of the [g][HD] partial (C = n / 4) and the splits
+    // s = t / C, t / C + R, ... (R = DT / C phases).
+    const int C = n / 4;
+    const int R = C >= DT ? 1 : DT / C;
+    float* red = lds;          // [R][n] per-phase sums (<= 2048 floats)
+    float* wts = lds + 2048;   // [nsplit][group] m then weights, [nsplit][group] l (<= 2048 floats)
+    // Weights: M_g = max_s m, w_sg = 2^(m_sg - M_g), L_g = sum_s l_sg w_sg.
+    for (int i = tid; i < nsplit * group; i += DT) {
+        wts[i] = ld_coherent(pml + 2 * i);
+        wts[nsplit * group + i] = ld_coherent(pml + 2 * i + 1);
+    }
+    __syncthreads();
+    if (tid < group) {
         float mx = ninf();
-        for (int s = lane; s < nsplit; s += 64) {
-            const float ms = all[((size_t)s * group + g) * rec + HD];
-            mx = fmaxf(mx, ms);
-        }
-#pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+        for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, wts[s * group + tid]);
         float L = 0.0f;
-        for (int s = lane; s < nsplit; s += 64) {
-            const float* pc = all + ((size_t)s * group + g) * rec;
-            const float w = ex2(pc[HD] - mx);
-            wts[g * DECODE_MAX_SPLITS + s] = w;
-            L += pc[HD + 1] * w;
+        for (int s = 0; s < nsplit; ++s) {
+            const float w = ex2(wts[s * group + tid] - mx);
+            wts[s * group + tid] = w;
+            L += wts[nsplit * group + s * group + tid] * w;
         }
-        // Fixed-order sum across lanes: butterfly is order-deterministic.
+        gl[tid] = L;
+    }
+    __syncthreads();
+    for (int w = tid; w < R * C; w += DT) {
+        const int c4 = w % C, phase = w / C;
+        const int g = (4 * c4) / HD;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        constexpr int U = 16;
+        for (int s0 = phase; s0 < nsplit; s0 += U * R) {
+            float4 x[U];
 #pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) L += __shfl_xor(L, o2, 64);
-        if (lane == 0) gl[g] = L;
+            for (int u = 0; u < U; ++u) {
+                const int s = s0 + u * R;
+                x[u] = s < nsplit ? ld_coherent4(po + (size_t)s * n + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s = s0 + u * R;
+                const float wt = s < nsplit ? wts[s * group + g] : 0.0f;
+                acc.x += x[u].x * wt;
+                acc.y += x[u].y * wt;
+                acc.z += x[u].z * wt;
+                acc.w += x[u].w * wt;
+            }
+        }
+        reinterpret_cast<float4*>(red + phase * n)[c4] = acc;
     }
     __syncthreads();
     for (int e = tid; e < n; e += DT) {
-        const int g = e / HD, d = e % HD;
         float acc = 0.0f;
-        for (int s = 0; s < nsplit; ++s)
-            acc += all[((size_t)s * group + g) * rec + d] * wts[g * DECODE_MAX_SPLITS + s];
-        emit(out, tc, ts, (size_t)h * group * HD + e, acc / gl[g]);
+        for (int r = 0; r < R; ++r) acc += red[r * n + e];
+        emit(out, tc, ts, (size_t)h * group * HD + e, acc / gl[e / HD]);
     }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-#define DECODE_INST(HD, KIND) \
-    template __global__ void attn_decode_kernel<HD, KIND>(DecodeArgs);
-DECODE_INST(64, KV_F16)
-DECODE_INST(128, KV_F16)
-DECODE_INST(64, KV_F32)
-DECODE_INST(128, KV_F32)
-DECODE_INST(64, KV_Q8)
-DECODE_INST(128, KV_Q8)
+#define DECODE_INST(HD, KIND, VA) template __global__ void attn_decode_kernel<HD, KIND, VA>(DecodeArgs);
+DECODE_INST(64, KV_F16, 16) DECODE_INST(128, KV_F16, 16) DECODE_INST(64, KV_F16, 8) DECODE_INST(128, KV_F16, 8)
+DECODE_INST(64, KV_F32, 16) DECODE_INST(128, KV_F32, 16) DECODE_INST(64, KV_F32, 8) DECODE_INST(128, KV_F32, 8)
+DECODE_INST(64, KV_T16, 16) DECODE_INST(128, KV_T16, 16) DECODE_INST(64, KV_TQ8, 16) DECODE_INST(128, KV_TQ8, 16)
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
     dim3 grid(a.splits, kv_heads, nseq), block(DT);
-#define L(HD, KIND) \
-    if (hd == HD && kind == KIND) { hipLaunchKernelGGL((attn_decode_kernel<HD, KIND>), grid, block, 0, st, a); return hipGetLastError(); }
-    L(64, KV_F16) L(128, KV_F16) L(64, KV_F32) L(128, KV_F32) L(64, KV_Q8) L(128, KV_Q8)
+    const int esz = kind == KV_F32 ? 4 : 2;
+    const int va = (kind == KV_T16 || kind == KV_TQ8) ? 16 : (((long)a.cap * esz) % 16 == 0 ? 16 : 8);
+#define L(HD, KIND, VA)                                                                        \
+    if (hd == HD && kind == KIND && va == VA) {                                                \
+        hipLaunchKernelGGL((attn_decode_kernel<HD, KIND, VA>), grid, block, 0, st, a);          \
+        return hipGetLastError();                                                              \
+    }
+    L(64, KV_F16, 16) L(128, KV_F16, 16) L(64, KV_F16, 8) L(128, KV_F16, 8)
+    L(64, KV_F32, 16) L(128, KV_F32, 16) L(64, KV_F32, 8) L(128, KV_F32, 8)
+    L(64, KV_T16, 16) L(128, KV_T16, 16) L(64, KV_TQ8, 16) L(128, KV_TQ8, 16)
 #undef L
     return hipErrorInvalidValue;
 }

@@ -12,6 +12,7 @@
 // over the source row, scattered into the destination layout.
 #include "common.h"
 #include "kvcache.h"
+#include "kvlayout.h"
 
 // No multiply-add contraction in this file: the rotations are the reference's
 // separate f32 multiplies and subtraction, so the fused rotate+append and the
@@ -119,11 +120,25 @@ __device__ __forceinline__ void q8_block(float x, int8_t& code, uint16_t& dbits)
     dbits = __builtin_bit_cast(uint16_t, to_h(d));
 }
 
-// n rows [n][kv*hd] of K (already rotated) and V into slot `slot` of the Q8_0
-// caches at positions past..past+n-1.
+// Byte offsets of element (position p, dim d) of (slot, kv head) `kvh` in a
+// tiled Q8_0 cache (kvlayout.h): codes and the scale of its dim block.
+struct Q8At {
+    long code, scale;
+};
+__device__ __forceinline__ Q8At q8_at(size_t kvh, int nblk, int hd, int p, int d, bool value) {
+    const long blk = ((long)kvh * nblk + (p >> 5)) * tq8_block_bytes(hd);
+    const int kk = p & 31;
+    Q8At r;
+    r.code = blk + (value ? 32L * hd + tq8_v_off(kk, d) : tq8_k_off(hd, kk, d));
+    r.scale = blk + 64L * hd + (value ? 64L * (hd / 32) : 0) + 2L * (kk * (hd / 32) + (d >> 5));
+    return r;
+}
+
+// n rows [n][kv*hd] of K (already rotated) and V into slot `slot` of a tiled
+// Q8_0 cache at positions past..past+n-1.
 __global__ __launch_bounds__(KB) void append_q8_kernel(const float* k, long k_off, const float* v, long v_off,
-                                                       int8_t* kc, uint16_t* ksc, int8_t* vc, uint16_t* vsc,
-                                                       int slot, int n, int kv, int hd, int cap, int past) {
+                                                       char* cache, int slot, int n, int kv, int hd, int cap,
+                                                       int past) {
     const long i = (long)blockIdx.x * KB + threadIdx.x;
     const int d = kv * hd;
     const long total = (long)n * d;
@@ -135,18 +150,20 @@ __global__ __launch_bounds__(KB) void append_q8_kernel(const float* k, long k_of
     const int hh = (int)((ii % d) / hd);
     const int j = (int)(ii % hd);
     const size_t kvh = (size_t)slot * kv + hh;
-    const int nb = hd / 32;
+    const int nb = tiled_nblk(cap);
     int8_t c;
     uint16_t db;
     q8_block(live ? k[k_off + ii] : 0.0f, c, db);
     if (live) {
-        kc[(kvh * cap + past + ti) * hd + j] = c;
-        if ((j & 31) == 0) ksc[(kvh * cap + past + ti) * nb + (j >> 5)] = db;
+        const Q8At at = q8_at(kvh, nb, hd, past + ti, j, false);
+        cache[at.code] = c;
+        if ((j & 31) == 0) *reinterpret_cast<uint16_t*>(cache + at.scale) = db;
     }
     q8_block(live ? v[v_off + ii] : 0.0f, c, db);
     if (live) {
-        vc[(kvh * hd + j) * cap + past + ti] = c;
-        if ((j & 31) == 0) vsc[(kvh * cap + past + ti) * nb + (j >> 5)] = db;
+        const Q8At at = q8_at(kvh, nb, hd, past + ti, j, true);
+        cache[at.code] = c;
+        if ((j & 31) == 0) *reinterpret_cast<uint16_t*>(cache + at.scale) = db;
     }
 }
 
@@ -157,8 +174,7 @@ __global__ __launch_bounds__(KB) void append_q8_kernel(const float* k, long k_of
 __global__ __launch_bounds__(KB) void rope_cache_q8_kernel(float* q, long q_off, const float* k, long k_off,
                                                            const float* v, long v_off, const float* div,
                                                            int heads, int kv, int hd, float theta, int pos,
-                                                           int8_t* kc, uint16_t* ksc, int8_t* vc, uint16_t* vsc,
-                                                           int slot, int cap) {
+                                                           char* cache, int slot, int cap) {
     const int half = hd >> 1;
     const int nq = heads * half;  // q pairs
     const int nk = kv * hd;       // rotated k elements
@@ -198,15 +214,81 @@ __global__ __launch_bounds__(KB) void rope_cache_q8_kernel(float* q, long q_off,
     uint16_t db;
     q8_block(x, c, db);
     if (!live) return;
-    const size_t kvh = (size_t)slot * kv + hh;
-    const int nb = hd / 32;
-    if (is_k) {
-        kc[(kvh * cap + pos) * hd + jj] = c;
-        if ((jj & 31) == 0) ksc[(kvh * cap + pos) * nb + (jj >> 5)] = db;
-    } else {
-        vc[(kvh * hd + jj) * cap + pos] = c;
-        if ((jj & 31) == 0) vsc[(kvh * cap + pos) * nb + (jj >> 5)] = db;
+    const Q8At at = q8_at((size_t)slot * kv + hh, tiled_nblk(cap), hd, pos, jj, !is_k);
+    cache[at.code] = c;
+    if ((jj & 31) == 0) *reinterpret_cast<uint16_t*>(cache + at.scale) = db;
+}
+
+// ------------------------------------------------------------ tiled f16
+
+// Half offset of element (position p, dim d) of kv head h in a tiled f16 cache.
+__device__ __forceinline__ long t16_at(int h, int nblk, int hd, int p, int d, bool value) {
+    const long blk = ((long)h * nblk + (p >> 5)) * 64L * hd;
+    return blk + (value ? 32L * hd + t16_v_off(p & 31, d) : t16_k_off(hd, p & 31, d));
+}
+
+// The tiled twin of cache_append_f16: n rows [n][kv*hd] into positions
+// past.. of the K (or, `value`, the V) area.
+__global__ __launch_bounds__(KB) void append_t16_kernel(const float* src, long src_off, uint16_t* cache, int n,
+                                                        int kv, int hd, int cap, int past, int value) {
+    const long i = (long)blockIdx.x * KB + threadIdx.x;
+    const int d = kv * hd;
+    if (i >= (long)n * d) return;
+    const int ti = (int)(i / d);
+    const int hh = (int)((i % d) / hd);
+    const int j = (int)(i % hd);
+    cache[t16_at(hh, tiled_nblk(cap), hd, past + ti, j, value)] =
+        __builtin_bit_cast(uint16_t, to_h(src[src_off + i]));
+}
+
+// The tiled twin of rope_cache_f16.
+__global__ __launch_bounds__(KB) void rope_cache_t16_kernel(float* q, long q_off, const float* k, long k_off,
+                                                            const float* v, long v_off, const float* div,
+                                                            int heads, int kv, int hd, float theta, int pos,
+                                                            uint16_t* cache, int cap) {
+    const int half = hd >> 1;
+    const int nq = heads * half, nk = kv * half, nv = kv * hd;
+    const int nb = tiled_nblk(cap);
+    const int i = blockIdx.x * KB + threadIdx.x;
+    if (i < nq + nk) {
+        const bool is_q = i < nq;
+        const int e = is_q ? i : i - nq;
+        const int j = e % half, hh = e / half;
+        float sn, cs;
+        rope_sc(j, hd, theta, div, pos, sn, cs);
+        if (is_q) {
+            const size_t b = (size_t)q_off + (size_t)hh * hd + j;
+            const float a0 = q[b], b0 = q[b + half];
+            q[b] = a0 * cs - b0 * sn;
+            q[b + half] = b0 * cs + a0 * sn;
+        } else {
+            const size_t b = (size_t)k_off + (size_t)hh * hd + j;
+            const float a0 = k[b], b0 = k[b + half];
+            cache[t16_at(hh, nb, hd, pos, j, false)] = __builtin_bit_cast(uint16_t, to_h(a0 * cs - b0 * sn));
+            cache[t16_at(hh, nb, hd, pos, j + half, false)] = __builtin_bit_cast(uint16_t, to_h(b0 * cs + a0 * sn));
+        }
+    } else if (i < nq + nk + nv) {
+        const int e = i - nq - nk;
+        const int hh = e / hd, j = e % hd;
+        cache[t16_at(hh, nb, hd, pos, j, true)] = __builtin_bit_cast(uint16_t, to_h(v[(size_t)v_off + e]));
     }
+}
+
+// Reference-layout f16 caches (K [kv][cap][hd], V [kv][hd][cap]) into the
+// tiled layout, positions 0..live-1 (the rest of the last block is zeroed).
+__global__ __launch_bounds__(KB) void ref_to_t16_kernel(const uint16_t* k, const uint16_t* v, uint16_t* cache, int kv,
+                                                        int hd, int cap, int live, int tcap) {
+    const long i = (long)blockIdx.x * KB + threadIdx.x;
+    const int nbl = (live + 31) / 32;
+    const long per = (long)nbl * 32 * hd;  // elements per head and area
+    if (i >= 2L * kv * per) return;
+    const bool value = i >= (long)kv * per;
+    const long e = value ? i - (long)kv * per : i;
+    const int hh = (int)(e / per);
+    const int p = (int)((e % per) / hd), d = (int)(e % hd);
+    uint16_t x = 0;
+    if (p < live) x = value ? v[((size_t)hh * hd + d) * cap + p] : k[((size_t)hh * cap + p) * hd + d];
+    cache[t16_at(hh, tiled_nblk(tcap), hd, p, d, value)] = x;
 }
 
 static inline unsigned nblk(long n) { return (unsigned)((n + KB - 1) / KB); }
@@ -252,23 +334,48 @@ hipError_t launch_grow(const void* src, void* dst, int esz, int rows, int len, i
     return hipGetLastError();
 }
 
-hipError_t launch_append_q8(const float* k, long k_off, const float* v, long v_off, int8_t* kc, uint16_t* ksc,
-                            int8_t* vc, uint16_t* vsc, int slot, int n, int kv, int hd, int cap, int past,
-                            hipStream_t st) {
+hipError_t launch_append_q8(const float* k, long k_off, const float* v, long v_off, char* cache, int slot, int n,
+                            int kv, int hd, int cap, int past, hipStream_t st) {
     const long tot = (long)n * kv * hd;
     if (tot == 0) return hipSuccess;
-    hipLaunchKernelGGL(append_q8_kernel, dim3(nblk(tot)), dim3(KB), 0, st, k, k_off, v, v_off, kc, ksc, vc, vsc,
-                       slot, n, kv, hd, cap, past);
+    hipLaunchKernelGGL(append_q8_kernel, dim3(nblk(tot)), dim3(KB), 0, st, k, k_off, v, v_off, cache, slot, n, kv, hd,
+                       cap, past);
     return hipGetLastError();
 }
 
 hipError_t launch_rope_cache_q8(float* q, long q_off, const float* k, long k_off, const float* v, long v_off,
-                                const float* div, int heads, int kv, int hd, float theta, int pos, int8_t* kc,
-                                uint16_t* ksc, int8_t* vc, uint16_t* vsc, int slot, int cap, hipStream_t st) {
+                                const float* div, int heads, int kv, int hd, float theta, int pos, char* cache,
+                                int slot, int cap, hipStream_t st) {
     const unsigned qb = nblk((long)heads * (hd / 2));
     const unsigned kb = nblk(2L * kv * hd);
     hipLaunchKernelGGL(rope_cache_q8_kernel, dim3(qb + kb), dim3(KB), 0, st, q, q_off, k, k_off, v, v_off, div,
-                       heads, kv, hd, theta, pos, kc, ksc, vc, vsc, slot, cap);
+                       heads, kv, hd, theta, pos, cache, slot, cap);
+    return hipGetLastError();
+}
+
+hipError_t launch_append_t16(const float* src, long src_off, uint16_t* cache, int n, int kv, int hd, int cap,
+                             int past, int value, hipStream_t st) {
+    const long tot = (long)n * kv * hd;
+    if (tot == 0) return hipSuccess;
+    hipLaunchKernelGGL(append_t16_kernel, dim3(nblk(tot)), dim3(KB), 0, st, src, src_off, cache, n, kv, hd, cap,
+                       past, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_cache_t16(float* q, long q_off, const float* k, long k_off, const float* v, long v_off,
+                                 const float* div, int heads, int kv, int hd, float theta, int pos, uint16_t* cache,
+                                 int cap, hipStream_t st) {
+    const long n = (long)heads * (hd / 2) + (long)kv * (hd / 2) + (long)kv * hd;
+    hipLaunchKernelGGL(rope_cache_t16_kernel, dim3(nblk(n)), dim3(KB), 0, st, q, q_off, k, k_off, v, v_off, div,
+                       heads, kv, hd, theta, pos, cache, cap);
+    return hipGetLastError();
+}
+
+hipError_t launch_ref_to_t16(const uint16_t* k, const uint16_t* v, uint16_t* cache, int kv, int hd, int cap, int live,
+                             int tcap, hipStream_t st) {
+    const long n = 2L * kv * ((live + 31) / 32) * 32 * hd;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(ref_to_t16_kernel, dim3(nblk(n)), dim3(KB), 0, st, k, v, cache, kv, hd, cap, live, tcap);
     return hipGetLastError();
 }
 

@@ -10,6 +10,7 @@ enum PfKind {
     PF_F16 = 0,   // f16 caches: K [kv][cap][hd], V [kv][hd][cap]
     PF_F32 = 1,   // the same layout at f32
     PF_ROWS = 2,  // columns of a stacked [t, 3d] f32 q/k/v product (Whisper encoder)
+    PF_T16 = 3,   // the tiled f16 cache of kvlayout.h (k = the cache, v unused)
 };
 
 struct PrefillArgs {

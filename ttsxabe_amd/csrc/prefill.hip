@@ -30,6 +30,7 @@
 // ds_read_b128 phase touches land on distinct banks.
 #include "common.h"
 #include "prefill.h"
+#include "kvlayout.h"
 
 namespace llmtie {
 
@@ -119,30 +120,78 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
     const size_t krs = rows ? (size_t)a.kvs : (size_t)HD;
     const bool kal = rows ? (a.kvs % 4 == 0) : true;
     const bool val = rows ? kal : (KIND == PF_F16 ? a.cap % 8 == 0 : a.cap % 4 == 0);
-    constexpr int SK = KIND == PF_ROWS ? PF_F32 : KIND;
+    constexpr int SK = KIND == PF_ROWS ? PF_F32 : (KIND == PF_T16 ? PF_F16 : KIND);
 
+    // Tiled cache: a 64-key tile is two blocks; each block's K and V areas are
+    // copied verbatim (16-byte chunk i of an area to LDS chunk i), so the
+    // fragment reads below are lane-contiguous and conflict-free. V chunks of
+    // keys >= ktot are zeroed (a tiled cache holds garbage there).
+    const size_t tblk = (size_t)kh * tiled_nblk(a.cap);  // first block of this kv head
     auto load_tile = [&](int kv0, St& st) {
+        if constexpr (KIND == PF_T16) {
+            constexpr int AREA = 32 * HD / 8;  // 16-byte chunks per area
 #pragma unroll
-        for (int i = 0; i < St::KC; ++i) {
-            const int id = tid + PT * i;
-            const int r = id / KCH, c = id % KCH;
-            st.k[i] = fetch8<HD, SK>(a.k, kbase + (size_t)(kv0 + r) * krs + 8 * c, kv0 + r < kend ? 8 : 0, kal);
-        }
+            for (int i = 0; i < St::KC; ++i) {
+                const int id = tid + PT * i;       // 0 .. 2*AREA-1 over the two blocks
+                const int hb = id / AREA, ci = id % AREA;
+                const int b0 = kv0 + 32 * hb;
+                const half8* src = reinterpret_cast<const half8*>(a.k) + (tblk + (b0 >> 5)) * (2 * AREA);
+                st.k[i] = b0 < ktot ? src[ci] : zero_h8();
+            }
 #pragma unroll
-        for (int i = 0; i < St::VC; ++i) {
-            const int id = tid + PT * i;
-            if constexpr (KIND == PF_ROWS) {
-                // V rows [key][d]: chunk = 8 dims of one key.
+            for (int i = 0; i < St::VC; ++i) {
+                const int id = tid + PT * i;
+                const int hb = id / AREA, ci = id % AREA;
+                const int b0 = kv0 + 32 * hb;
+                const half8* src = reinterpret_cast<const half8*>(a.k) + (tblk + (b0 >> 5)) * (2 * AREA) + AREA;
+                half8 x = zero_h8();
+                if (b0 < ktot) {
+                    x = src[ci];
+                    const int k0 = b0 + 8 * ((ci & 63) >> 4);  // keys of this chunk: k0 .. k0 + 7
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if (k0 + j >= ktot) x[j] = (half_t)0.0f;
+                }
+                st.v[i] = x;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < St::KC; ++i) {
+                const int id = tid + PT * i;
                 const int r = id / KCH, c = id % KCH;
-                st.v[i] = fetch8<HD, SK>(a.v, vbase + (size_t)(kv0 + r) * krs + 8 * c, kv0 + r < kend ? 8 : 0, val);
-            } else {
-                const int d = id / (KT / 8), c = id % (KT / 8);
-                const int p = kv0 + 8 * c;
-                st.v[i] = fetch8<HD, SK>(a.v, vbase + (size_t)d * a.cap + p, min(8, kend - p), val);
+                st.k[i] = fetch8<HD, SK>(a.k, kbase + (size_t)(kv0 + r) * krs + 8 * c, kv0 + r < kend ? 8 : 0, kal);
+            }
+#pragma unroll
+            for (int i = 0; i < St::VC; ++i) {
+                const int id = tid + PT * i;
+                if constexpr (KIND == PF_ROWS) {
+                    // V rows [key][d]: chunk = 8 dims of one key.
+                    const int r = id / KCH, c = id % KCH;
+                    st.v[i] = fetch8<HD, SK>(a.v, vbase + (size_t)(kv0 + r) * krs + 8 * c, kv0 + r < kend ? 8 : 0, val);
+                } else {
+                    const int d = id / (KT / 8), c = id % (KT / 8);
+                    const int p = kv0 + 8 * c;
+                    st.v[i] = fetch8<HD, SK>(a.v, vbase + (size_t)d * a.cap + p, min(8, kend - p), val);
+                }
             }
         }
     };
     auto store_tile = [&](const St& st) {
+        if constexpr (KIND == PF_T16) {
+            constexpr int AREA = 32 * HD / 8;
+#pragma unroll
+            for (int i = 0; i < St::KC; ++i) {
+                const int id = tid + PT * i;
+                reinterpret_cast<half8*>(ks)[id] = st.k[i];  // block hb's K area at [hb * AREA]
+            }
+#pragma unroll
+            for (int i = 0; i < St::VC; ++i) {
+                const int id = tid + PT * i;
+                reinterpret_cast<half8*>(vs)[id] = st.v[i];
+            }
+            (void)AREA;
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < St::KC; ++i) {
             const int id = tid + PT * i;
@@ -163,6 +212,23 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
                 const int d = id / (KT / 8), c = id % (KT / 8);
                 *reinterpret_cast<half8*>(&vs[d * KT + 8 * swz_v(d, c)]) = st.v[i];
             }
+        }
+    };
+    // Fragment reads: A operand of S^T for (half, T, step) and of O^T for (half, tile).
+    auto kfrag = [&](int hf, int T, int s) -> half8 {
+        if constexpr (KIND == PF_T16) {
+            return reinterpret_cast<const half8*>(ks)[hf * (32 * HD / 8) + (T * NS + s) * 64 + lane];
+        } else {
+            const int r = 32 * hf + 8 * (col >> 2) + 4 * T + (col & 3);
+            return *reinterpret_cast<const half8*>(&ks[r * HD + 8 * swz_k<HD>(r, 4 * s + grp)]);
+        }
+    };
+    auto vfrag = [&](int hf, int t) -> half8 {
+        if constexpr (KIND == PF_T16) {
+            return reinterpret_cast<const half8*>(vs)[hf * (32 * HD / 8) + t * 64 + lane];
+        } else {
+            const int d = 16 * t + col;
+            return *reinterpret_cast<const half8*>(&vs[d * KT + 8 * swz_v(d, 4 * hf + grp)]);
         }
     };
 
@@ -217,10 +283,9 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
             for (int T = 0; T < 2; ++T) {
 #pragma unroll
                 for (int u = 0; u < NQT; ++u) sc[hf][T][u] = zero_f4();
-                const int r = 32 * hf + 8 * (col >> 2) + 4 * T + (col & 3);
 #pragma unroll
                 for (int s = 0; s < NS; ++s) {
-                    const half8 af = *reinterpret_cast<const half8*>(&ks[r * HD + 8 * swz_k<HD>(r, 4 * s + grp)]);
+                    const half8 af = kfrag(hf, T, s);
 #pragma unroll
                     for (int u = 0; u < NQT; ++u) sc[hf][T][u] = mfma16(af, qb[u][s], sc[hf][T][u]);
                 }
@@ -273,8 +338,7 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const int d = 16 * t + col;
-                const half8 af = *reinterpret_cast<const half8*>(&vs[d * KT + 8 * swz_v(d, 4 * hf + grp)]);
+                const half8 af = vfrag(hf, t);
 #pragma unroll
                 for (int u = 0; u < NQT; ++u) o[t][u] = mfma16(af, pb[hf][u], o[t][u]);
             }
@@ -312,7 +376,7 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
         return hipGetLastError();                                                            \
     }
 #define LK(HD, KIND) L(HD, KIND, 1) L(HD, KIND, 2) L(HD, KIND, 4)
-    LK(64, PF_F16) LK(128, PF_F16) LK(64, PF_F32) LK(128, PF_F32) LK(64, PF_ROWS)
+    LK(64, PF_F16) LK(128, PF_F16) LK(64, PF_F32) LK(128, PF_F32) LK(64, PF_ROWS) LK(64, PF_T16) LK(128, PF_T16)
 #undef LK
 #undef L
     return hipErrorInvalidValue;

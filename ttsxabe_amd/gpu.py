@@ -23,7 +23,7 @@ from . import _lib
 __all__ = [
     "CudaError", "UnsupportedAttention", "OddCacheCapacity", "CacheOverrun", "SliceOverrun", "RaggedBlock",
     "MismatchedQ8", "OddHeadDim", "Driver", "NoDevice", "InvalidArgument", "DecodeScratch", "Q8", "KvCacheQ8",
-    "Gpu",
+    "TiledCache16", "Gpu",
 ]
 
 
@@ -162,19 +162,29 @@ class Q8:
 
 
 class KvCacheQ8:
-    """A GGUF Q8_0 KV cache for `slots` sequences (layout in llmtie_hip.h)."""
+    """A tiled GGUF Q8_0 KV cache for `slots` sequences (layout in
+    llmtie_hip.h / csrc/kvlayout.h): one int8 buffer of whole 32-position
+    blocks, codes and f16 scales of K and V per block."""
 
     def __init__(self, slots: int, kv_heads: int, head_dim: int, cap: int, device="cuda"):
         self.slots, self.kv_heads, self.head_dim, self.cap = slots, kv_heads, head_dim, cap
-        n = slots * kv_heads * cap * head_dim
-        self.k_codes = torch.zeros(n, dtype=torch.int8, device=device)
-        self.v_codes = torch.zeros(n, dtype=torch.int8, device=device)
-        self.k_scales = torch.zeros(n // 32, dtype=torch.float16, device=device)
-        self.v_scales = torch.zeros(n // 32, dtype=torch.float16, device=device)
+        n = _lib.lib().llmtie_q8_cache_bytes(slots, kv_heads, head_dim, cap)
+        self.data = torch.zeros(n, dtype=torch.int8, device=device)
 
     def bytes_per_position(self) -> int:
         """HBM bytes one live position of one sequence costs a decode step."""
         return 2 * self.kv_heads * (self.head_dim + 2 * self.head_dim // 32)
+
+
+class TiledCache16:
+    """A tiled f16 KV cache for one layer: K and V of every kv head in one
+    buffer, 32-position blocks in MFMA fragment order."""
+
+    def __init__(self, kv_heads: int, head_dim: int, cap: int, device="cuda", zero=True):
+        self.kv_heads, self.head_dim, self.cap = kv_heads, head_dim, cap
+        n = _lib.lib().llmtie_t16_cache_len(kv_heads, head_dim, cap)
+        alloc = torch.zeros if zero else torch.empty
+        self.data = alloc(n, dtype=torch.float16, device=device)
 
 
 class Gpu:
@@ -291,10 +301,70 @@ class Gpu:
         if out is None:
             out = torch.empty(max(nseq * n, 1), dtype=torch.float32, device=self.device)
         _check(self._L.llmtie_attn_decode_q8_batch(
-            self._stream(), _p(q), _n(q), _p(cache.k_codes), _p(cache.k_scales), _p(cache.v_codes),
-            _p(cache.v_scales), cache.slots, _p(tk_dev), _p(slot_dev), nseq, max_tk, heads, cache.kv_heads,
-            cache.head_dim, cache.cap, C.c_float(scale), int(bool(scale_q)), scratch.handle, _p(out), _n(out)))
+            self._stream(), _p(q), _n(q), _p(cache.data), _n(cache.data), cache.slots, _p(tk_dev), _p(slot_dev),
+            nseq, max_tk, heads, cache.kv_heads, cache.head_dim, cache.cap, C.c_float(scale), int(bool(scale_q)),
+            scratch.handle, _p(out), _n(out)))
         return out[: nseq * n]
+
+    # ---------------------------------------------------------- tiled f16
+
+    def attn_decode_t16(self, q, cache: TiledCache16, heads, tk, scale, scale_q, scratch, out=None):
+        """attn_decode_f16 (device.rs:5949) off a tiled cache."""
+        _need(q, _F32, "q")
+        n = heads * cache.head_dim
+        if out is None:
+            out = torch.empty(n, dtype=torch.float32, device=self.device)
+        _check(self._L.llmtie_attn_decode_t16(self._stream(), _p(q), _n(q), _p(cache.data), _n(cache.data), heads,
+                                              cache.kv_heads, cache.head_dim, tk, cache.cap, C.c_float(scale),
+                                              int(bool(scale_q)), scratch.handle, _p(out), _n(out)))
+        return out
+
+    def attn_decode_t16_q_row(self, q, q_off, cache: TiledCache16, heads, tk, scale, scale_q, scratch, out,
+                              twin: Q8 = None, row=0):
+        """attn_decode_f16_q_row (device.rs:6001) off a tiled cache."""
+        _need(q, _F32, "q")
+        _need(out, _F32, "out")
+        _check(self._L.llmtie_attn_decode_t16_q_row(
+            self._stream(), _p(q), _n(q), q_off, _p(cache.data), _n(cache.data), heads, cache.kv_heads,
+            cache.head_dim, tk, cache.cap, C.c_float(scale), int(bool(scale_q)), scratch.handle, _p(out), _n(out),
+            None if twin is None else _p(twin.buf), 0 if twin is None else twin.rows,
+            0 if twin is None else twin.k, row))
+
+    def flash_attn_t16(self, q, cache: TiledCache16, tq, past, heads, scale, causal):
+        """flash_attn_f16 (device.rs:5754) off a tiled cache."""
+        _need(q, _F32, "q")
+        n = tq * heads * cache.head_dim
+        out = torch.empty(max(n, 1), dtype=torch.float32, device=self.device)
+        _check(self._L.llmtie_flash_attn_t16(self._stream(), _p(q), _n(q), _p(cache.data), _n(cache.data), _p(out),
+                                             n, tq, past, heads, cache.kv_heads, cache.head_dim, cache.cap,
+                                             C.c_float(scale), int(bool(causal))))
+        return out[:n]
+
+    def t16_append(self, src, src_off, cache: TiledCache16, n, past, value):
+        """cache_append_f16 (device.rs:2849) into a tiled cache; value selects V."""
+        _need(src, _F32, "src")
+        _check(self._L.llmtie_t16_append(self._stream(), _p(src), _n(src), src_off, _p(cache.data), _n(cache.data),
+                                         n, cache.kv_heads, cache.head_dim, cache.cap, past, int(bool(value))))
+
+    def t16_rope_cache(self, q, q_off, k, k_off, v, v_off, freq_div, heads, theta, pos, cache: TiledCache16):
+        """rope_cache_f16 (device.rs:2915) into a tiled cache."""
+        for t, w in ((q, "q"), (k, "k"), (v, "v"), (freq_div, "freq_div")):
+            _need(t, _F32, w)
+        _check(self._L.llmtie_t16_rope_cache(self._stream(), _p(q), _n(q), q_off, _p(k), _n(k), k_off, _p(v), _n(v),
+                                             v_off, _p(freq_div), heads, cache.kv_heads, cache.head_dim,
+                                             C.c_float(theta), pos, _p(cache.data), _n(cache.data), cache.cap))
+
+    def t16_grow(self, src: TiledCache16, dst: TiledCache16, live):
+        """cache_grow_f16 (device.rs:3152) between tiled caches."""
+        _check(self._L.llmtie_t16_grow(self._stream(), _p(src.data), _n(src.data), _p(dst.data), _n(dst.data),
+                                       src.kv_heads, src.head_dim, src.cap, dst.cap, live))
+
+    def t16_from_ref(self, k, v, cache: TiledCache16, live):
+        """Repack reference-layout f16 caches into a tiled one."""
+        _need(k, _H16, "k")
+        _need(v, _H16, "v")
+        _check(self._L.llmtie_t16_from_ref(self._stream(), _p(k), _n(k), _p(v), _n(v), cache.kv_heads,
+                                           cache.head_dim, cache.cap, live, _p(cache.data), _n(cache.data)))
 
     # ----------------------------------------------------------- producers
 
@@ -353,9 +423,8 @@ class Gpu:
         """Quantize n rows of k and v into slot `slot` at positions past.. (new)."""
         _need(k, _F32, "k")
         _need(v, _F32, "v")
-        _check(self._L.llmtie_kv_q8_append(self._stream(), _p(k), _n(k), k_off, _p(v), _n(v), v_off,
-                                           _p(cache.k_codes), _p(cache.k_scales), _p(cache.v_codes),
-                                           _p(cache.v_scales), cache.slots, slot, n, cache.kv_heads, cache.head_dim,
+        _check(self._L.llmtie_kv_q8_append(self._stream(), _p(k), _n(k), k_off, _p(v), _n(v), v_off, _p(cache.data),
+                                           _n(cache.data), cache.slots, slot, n, cache.kv_heads, cache.head_dim,
                                            cache.cap, past))
 
     def rope_cache_q8(self, q, q_off, k, k_off, v, v_off, freq_div, heads, theta, pos, cache: KvCacheQ8, slot):
@@ -364,5 +433,5 @@ class Gpu:
             _need(t, _F32, w)
         _check(self._L.llmtie_rope_cache_q8(self._stream(), _p(q), _n(q), q_off, _p(k), _n(k), k_off, _p(v), _n(v),
                                             v_off, _p(freq_div), heads, cache.kv_heads, cache.head_dim,
-                                            C.c_float(theta), pos, _p(cache.k_codes), _p(cache.k_scales),
-                                            _p(cache.v_codes), _p(cache.v_scales), cache.slots, slot, cache.cap))
+                                            C.c_float(theta), pos, _p(cache.data), _n(cache.data), cache.slots, slot,
+                                            cache.cap))
