@@ -98,50 +98,79 @@ def rand_f16(torch, n, gen):
     return torch.randn(n, generator=gen, device="cuda", dtype=torch.float32).to(torch.float16)
 
 
-def bench_decode_f16(torch, g, heads, kv, hd, tk, cap, scale_q, steps, warmup, layers, f32_cache=False):
-    from ttsxabe_amd.gpu import DecodeScratch
+def bench_decode_f16(torch, g, heads, kv, hd, tk, cap, scale_q, steps, warmup, layers, f32_cache=False,
+                     tiled=False):
+    """One decode launch per layer over distinct per-layer caches. tiled: the
+    fragment-order f16 cache (llmtie_attn_decode_t16); else the reference
+    layout (llmtie_attn_decode_f16 / llmtie_attn_decode)."""
+    from ttsxabe_amd.gpu import DecodeScratch, TiledCache16
     gen = torch.Generator(device="cuda").manual_seed(1234)
     esz = 4 if f32_cache else 2
     bytes_layer = 2 * kv * tk * hd * esz
     L = rotate_layers(2 * kv * cap * hd * esz, layers)
-    if f32_cache:
-        ks = [torch.randn(kv * cap * hd, generator=gen, device="cuda") for _ in range(L)]
-        vs = [torch.randn(kv * cap * hd, generator=gen, device="cuda") for _ in range(L)]
-    else:
-        ks = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
-        vs = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
     qs = [torch.randn(heads * hd, generator=gen, device="cuda") for _ in range(L)]
     scratch = DecodeScratch()
-    fn_ = g.attn_decode if f32_cache else g.attn_decode_f16
     scale = hd ** -0.5
+    if tiled:
+        caches = []
+        for _ in range(L):
+            c = TiledCache16(kv, hd, cap, zero=False)
+            c.data.copy_(rand_f16(torch, c.data.numel(), gen))
+            caches.append(c)
 
-    def step():
-        return [fn_(qs[l], ks[l], vs[l], heads, kv, hd, tk, cap, scale, scale_q, scratch) for l in range(L)]
+        def step():
+            return [g.attn_decode_t16(qs[l], caches[l], heads, tk, scale, scale_q, scratch) for l in range(L)]
+    else:
+        if f32_cache:
+            ks = [torch.randn(kv * cap * hd, generator=gen, device="cuda") for _ in range(L)]
+            vs = [torch.randn(kv * cap * hd, generator=gen, device="cuda") for _ in range(L)]
+        else:
+            ks = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
+            vs = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
+        fn_ = g.attn_decode if f32_cache else g.attn_decode_f16
+
+        def step():
+            return [fn_(qs[l], ks[l], vs[l], heads, kv, hd, tk, cap, scale, scale_q, scratch) for l in range(L)]
 
     ms = Timer(torch, step).time(steps, warmup)
     per_launch_us = ms * 1e3 / L
     gbs = bytes_layer / (per_launch_us * 1e-6) / 1e9
-    return dict(layers=L, ms_per_step=ms, us_per_launch=per_launch_us, bytes_per_launch=bytes_layer, gbs=gbs,
+    return dict(layers=L, layout="tiled f16" if tiled else ("reference f32" if f32_cache else "reference f16"),
+                ms_per_step=ms, us_per_launch=per_launch_us, bytes_per_launch=bytes_layer, gbs=gbs,
                 frac=gbs / HBM_PEAK_GBS)
 
 
-def bench_prefill(torch, g, tq, heads, kv, hd, steps, warmup, layers):
+def bench_prefill(torch, g, tq, heads, kv, hd, steps, warmup, layers, tiled=True):
+    """Causal GQA prefill of tq tokens, one launch per layer over distinct
+    per-layer caches (tiled: llmtie_flash_attn_t16; else llmtie_flash_attn_f16)."""
+    from ttsxabe_amd.gpu import TiledCache16
     gen = torch.Generator(device="cuda").manual_seed(99)
     cap = tq
     flop = 4 * hd * heads * (tq * (tq + 1) // 2)  # bench_flash.rs:107-112, causal
     L = max(1, min(layers, rotate_layers(2 * kv * cap * hd * 2 + 2 * tq * heads * hd * 4, layers)))
     qs = [torch.randn(tq * heads * hd, generator=gen, device="cuda") for _ in range(L)]
-    ks = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
-    vs = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
     scale = hd ** -0.5
+    if tiled:
+        caches = []
+        for _ in range(L):
+            c = TiledCache16(kv, hd, cap, zero=False)
+            c.data.copy_(rand_f16(torch, c.data.numel(), gen))
+            caches.append(c)
 
-    def step():
-        return [g.flash_attn_f16(qs[l], ks[l], vs[l], tq, 0, heads, kv, hd, cap, scale, True) for l in range(L)]
+        def step():
+            return [g.flash_attn_t16(qs[l], caches[l], tq, 0, heads, scale, True) for l in range(L)]
+    else:
+        ks = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
+        vs = [rand_f16(torch, kv * cap * hd, gen) for _ in range(L)]
+
+        def step():
+            return [g.flash_attn_f16(qs[l], ks[l], vs[l], tq, 0, heads, kv, hd, cap, scale, True) for l in range(L)]
 
     ms = Timer(torch, step).time(steps, warmup)
     us = ms * 1e3 / L
     tf = flop / (us * 1e-6) / 1e12
-    return dict(tq=tq, layers=L, us_per_launch=us, flop_per_launch=flop, tflops=tf, frac=tf / F16_PEAK_TFLOPS)
+    return dict(tq=tq, layers=L, layout="tiled f16" if tiled else "reference f16", us_per_launch=us,
+                flop_per_launch=flop, tflops=tf, frac=tf / F16_PEAK_TFLOPS)
 
 
 def bench_encoder(torch, g, t, heads, hd, steps, warmup, layers):
@@ -162,6 +191,8 @@ def bench_encoder(torch, g, t, heads, hd, steps, warmup, layers):
 
 
 def bench_q8_batch(torch, g, steps, warmup):
+    """C5: 32 sequences, one launch over a tiled Q8_0 cache; lengths from the
+    seeded U[256, 8192] draw; two layers' caches alternate (> 2x the LLC)."""
     from ttsxabe_amd.gpu import DecodeScratch, KvCacheQ8
     from tests import configs
     nseq, heads, kv, hd, cap = 32, 32, 8, 128, 8192
@@ -170,12 +201,15 @@ def bench_q8_batch(torch, g, steps, warmup):
     L = max(2, math.ceil(2 * LLC_BYTES / bytes_layer))
     gen = torch.Generator(device="cuda").manual_seed(5)
     caches = []
+    nb = hd // 32
     for _ in range(L):
         c = KvCacheQ8(nseq, kv, hd, cap)
-        c.k_codes.copy_(torch.randint(-127, 128, c.k_codes.shape, generator=gen, device="cuda", dtype=torch.int8))
-        c.v_codes.copy_(torch.randint(-127, 128, c.v_codes.shape, generator=gen, device="cuda", dtype=torch.int8))
-        c.k_scales.copy_((torch.randn(c.k_scales.shape, generator=gen, device="cuda").abs() * 0.02).half())
-        c.v_scales.copy_((torch.randn(c.v_scales.shape, generator=gen, device="cuda").abs() * 0.02).half())
+        nblocks = nseq * kv * (cap // 32)
+        blocks = c.data.view(nblocks, -1)
+        blocks[:, : 64 * hd].copy_(torch.randint(-128, 128, (nblocks, 64 * hd), generator=gen, device="cuda",
+                                                 dtype=torch.int8))
+        sc = (torch.randn(nblocks, 64 * nb, generator=gen, device="cuda").abs() * 0.02).half()
+        blocks[:, 64 * hd:].copy_(sc.view(torch.int8))
         caches.append(c)
     q = [torch.randn(nseq * heads * hd, generator=gen, device="cuda") for _ in range(L)]
     tk_d = torch.from_numpy(tk).to("cuda")
@@ -253,7 +287,7 @@ def main():
     from ttsxabe_amd.gpu import Gpu
     g = Gpu(0)
     print("bench: C2 decode", file=sys.stderr, flush=True)
-    c2 = bench_decode_f16(torch, g, 32, 8, 128, 4096, 4096, False, a.steps, a.warmup, a.layers)
+    c2 = bench_decode_f16(torch, g, 32, 8, 128, 4096, 4096, False, a.steps, a.warmup, a.layers, tiled=True)
     line = {
         "metric": "decode attn HBM GB/s + prefill attn TFLOP/s (% roofline), 1×MI355X",
         "value": round(c2["gbs"], 2),
@@ -268,13 +302,14 @@ def main():
         "dtype": "f16",
         "data": "synthetic (seeded N(0,1) f16 KV caches, f32 queries)",
         "config": {"workload": "C2: Llama-3-8B GQA decode, 32 q / 8 kv heads, head_dim 128, 4096-position f16 "
-                               "KV cache, batch 1; one step = one token through %d layers (distinct caches, "
-                               "HIP-graph replay)" % c2["layers"],
+                               "KV cache (tiled fragment-order layout), batch 1; one step = one token through %d "
+                               "layers (distinct caches, HIP-graph replay)" % c2["layers"],
                    "heads": 32, "kv_heads": 8, "head_dim": 128, "context": 4096, "layers": c2["layers"],
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(c2["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(c2["frac"], 4), "traffic": traffic_from_profiles("attn_decode_c2_counters.md"),
-                     "kernel": "attn_decode_kernel<128, KV_F16>", "bytes_per_launch": c2["bytes_per_launch"],
+                     "kernel": "attn_decode_kernel<128, KV_T16> (+ attn_merge_kernel)",
+                     "bytes_per_launch": c2["bytes_per_launch"],
                      "us_per_launch": round(c2["us_per_launch"], 3)},
     }
     if not a.no_secondary:
@@ -283,11 +318,17 @@ def main():
         print("bench: C3 prefill", file=sys.stderr, flush=True)
         for tq in (512, 128):
             sec[f"c3_prefill_{tq}"] = bench_prefill(torch, g, tq, 32, 8, 128, steps, a.warmup, a.layers)
+        sec["c3_prefill_512_reference_layout"] = bench_prefill(torch, g, 512, 32, 8, 128, steps, a.warmup, a.layers,
+                                                               tiled=False)
         sec["c3_prefill_8192_steady"] = bench_prefill(torch, g, 8192, 32, 8, 128, max(3, steps // 5), 2, 1)
+        sec["c2_decode_reference_layout"] = bench_decode_f16(torch, g, 32, 8, 128, 4096, 4096, False, steps,
+                                                             a.warmup, a.layers)
         print("bench: C4", file=sys.stderr, flush=True)
         sec["c4_encoder"] = bench_encoder(torch, g, 1500, 20, 64, steps, a.warmup, a.layers)
         sec["c4_cross_decode"] = bench_decode_f16(torch, g, 20, 20, 64, 1500, 1500, True, steps, a.warmup,
-                                                  a.layers)
+                                                  a.layers, tiled=True)
+        sec["c4_cross_decode_reference_layout"] = bench_decode_f16(torch, g, 20, 20, 64, 1500, 1500, True, steps,
+                                                                   a.warmup, a.layers)
         sec["c4_self_decode_224_f32"] = bench_decode_f16(torch, g, 20, 20, 64, 224, 448, True, steps, a.warmup,
                                                          a.layers, f32_cache=True)
         print("bench: C5", file=sys.stderr, flush=True)
@@ -296,6 +337,8 @@ def main():
             for k2 in list(v):
                 if isinstance(v[k2], float):
                     v[k2] = round(v[k2], 4)
+        # The peak the secondary numbers are fractions of, for reading them.
+        sec["peaks"] = {"hbm_gbs": HBM_PEAK_GBS, "f16_mfma_tflops": F16_PEAK_TFLOPS}
         line["secondary"] = sec
     if not a.no_cpu:
         print("bench: CPU baseline", file=sys.stderr, flush=True)

@@ -98,8 +98,12 @@ def pack_q8(kc, ks, vc, vs, slots: int, kv: int, hd: int, cap: int) -> np.ndarra
     bb = q8_block_bytes(hd)
     out = np.zeros((slots * kv, nblk, bb), np.uint8)
     for b in range(nblk):
-        out[:, b, :32 * hd] = kc[:, 32 * b + key_k, dim_k].view(np.uint8)
-        out[:, b, 32 * hd:64 * hd] = vc[:, dim_v, 32 * b + key_v].view(np.uint8)
-        out[:, b, 64 * hd:64 * hd + 64 * nb] = ks[:, 32 * b:32 * b + 32].reshape(-1, 32 * nb).view(np.uint8)
-        out[:, b, 64 * hd + 64 * nb:] = vs[:, 32 * b:32 * b + 32].reshape(-1, 32 * nb).view(np.uint8)
+        # codes offset-binary: the sign bit flipped
+        out[:, b, :32 * hd] = kc[:, 32 * b + key_k, dim_k].view(np.uint8) ^ 0x80
+        out[:, b, 32 * hd:64 * hd] = vc[:, dim_v, 32 * b + key_v].view(np.uint8) ^ 0x80
+        # scales dim-block-major: [nb][32 keys]
+        out[:, b, 64 * hd:64 * hd + 64 * nb] = np.ascontiguousarray(
+            ks[:, 32 * b:32 * b + 32].transpose(0, 2, 1)).reshape(-1, 32 * nb).view(np.uint8)
+        out[:, b, 64 * hd + 64 * nb:] = np.ascontiguousarray(
+            vs[:, 32 * b:32 * b + 32].transpose(0, 2, 1)).reshape(-1, 32 * nb).view(np.uint8)
     return out.ravel().view(np.int8)

@@ -160,7 +160,11 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
 // wave taking whole 32-key blocks, and never more than the merge can hold.
 void plan_decode(size_t tk_max, size_t units, size_t group, int& nit, int& splits) {
     const size_t max_splits = std::min<size_t>(DECODE_MAX_SPLITS, DECODE_MAX_SPLIT_ROWS / std::max<size_t>(1, group));
-    size_t target = 512;
+    // Measured on MI355X: a lone sequence decodes fastest over ~128
+    // workgroups (the split merge's cost grows with the count faster than the
+    // stream gains); a batch wants about three splits per (sequence, kv head)
+    // at its longest context so the long sequences do not set the time alone.
+    size_t target = std::max<size_t>(128, 3 * units);
     if (const char* e = getenv("LLMTIE_DECODE_WGS")) target = std::max(1, atoi(e));
     const size_t blocks = (tk_max + 31) / 32;
     size_t want = std::max<size_t>(1, target / std::max<size_t>(1, units));
@@ -174,6 +178,15 @@ void plan_decode(size_t tk_max, size_t units, size_t group, int& nit, int& split
     }
     nit = (int)n;
     splits = (int)((tk_max + span - 1) / span);
+}
+
+// Whether the split partials are merged by a second launch rather than by
+// the last-arriving workgroup of each head.
+int two_phase_merge(int splits, size_t units) {
+    if (const char* e = getenv("LLMTIE_DECODE_TWO_PHASE")) return atoi(e) ? 1 : 0;
+    // Past ~192 workgroups the in-launch hand-off (coherent stores, a wait,
+    // an atomic per workgroup) costs more than a second launch does.
+    return (size_t)splits * units >= 192 ? 1 : 0;
 }
 
 int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hipStream_t st) {
@@ -278,6 +291,7 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     a.qscale = scale_q ? scale : 1.0f;
     a.nit = nit;
     a.splits = splits;
+    a.two_phase = two_phase_merge(splits, kv_heads);
     return launched("attn_decode", launch_decode((int)hd, kind, a, (int)kv_heads, 1, S(stream)));
 }
 
@@ -411,6 +425,7 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     a.qscale = scale_q ? scale : 1.0f;
     a.nit = nit;
     a.splits = splits;
+    a.two_phase = two_phase_merge(splits, kv_heads * nseq);
     return launched("attn_decode_q8_batch", launch_decode((int)head_dim, KV_TQ8, a, (int)kv_heads, (int)nseq, S(stream)));
 }
 

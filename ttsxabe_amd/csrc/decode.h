@@ -35,6 +35,7 @@ struct DecodeArgs {
     float qscale;            // applied to q before it is split
     int nit;                 // 32-key blocks per wave per split
     int splits;              // grid.x: splits of the longest sequence
+    int two_phase;           // merge in a second launch (else the last split's workgroup merges)
 };
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);

@@ -46,21 +46,31 @@ namespace llmtie {
 constexpr int DW = 4;                 // waves per workgroup
 constexpr int DT = DW * LLMTIE_WAVE;  // threads per workgroup
 
-// Eight int8 codes (two dwords) as eight exact halves: flip the sign bit to
-// get c + 128, splice each byte under the exponent byte 0x64 (the half
-// 1024 + (c + 128)), and subtract 1152 with one packed f16 add per pair.
+// Eight offset-binary codes u = code + 128 (two dwords) as the halves
+// 1152 + code: each byte spliced under the exponent byte 0x64 is the half
+// 1024 + u. Exact, and two instructions per pair.
+__device__ __forceinline__ half8 dq8_biased(uint32_t w0, uint32_t w1) {
+    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u)};
+    half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[2 * i] = __builtin_bit_cast(half_t, (uint16_t)(p[i] & 0xffffu));
+        r[2 * i + 1] = __builtin_bit_cast(half_t, (uint16_t)(p[i] >> 16));
+    }
+    return r;
+}
+// The same with the 1152 taken off (one packed f16 add per pair): the codes.
 __device__ __forceinline__ half8 dq8(uint32_t w0, uint32_t w1) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
-    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u),
-                           __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)};
+    const half8 b = dq8_biased(w0, w1);
     const h2 bias = {(half_t)1152.0f, (half_t)1152.0f};
     half8 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const h2 v = __builtin_bit_cast(h2, p[i]) - bias;
+        const h2 v = h2{b[2 * i], b[2 * i + 1]} - bias;
         r[2 * i] = v[0];
         r[2 * i + 1] = v[1];
     }
@@ -90,7 +100,7 @@ template <int HD>
 struct Frag<HD, KV_TQ8> {
     uint4 kc[2][HD / 64];  // (T, step pair)
     uint4 vc[HD / 32];     // tile pair
-    uint4 ks[HD / 32];     // keys 8g .. 8g+7 x all dim blocks, key-major
+    uint4 ks[HD / 32];     // per dim block: the scales of keys 8g .. 8g+7
     uint4 vs[HD / 32];
 };
 
@@ -178,11 +188,11 @@ __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<
             for (int sp = 0; sp < NS / 2; ++sp) f.kc[T][sp] = kc[(T * (NS / 2) + sp) * 64 + lane];
 #pragma unroll
         for (int tp = 0; tp < NT / 2; ++tp) f.vc[tp] = vc[tp * 64 + lane];
-        // Keys 8*grp .. +7, all NS dim blocks: NS 16-byte pieces per lane.
+        // Dim block i, keys 8*grp .. +7: one 16-byte piece per block.
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-            f.ks[i] = ks[grp * NS + i];
-            f.vs[i] = vs[grp * NS + i];
+            f.ks[i] = ks[i * 4 + grp];
+            f.vs[i] = vs[i * 4 + grp];
         }
     } else {
 #pragma unroll
@@ -255,7 +265,8 @@ __device__ __forceinline__ half_t h_at(const uint4& u, int e) {
 // >= tk are dropped (only the partial block needs it).
 template <int HD, int KIND, bool MASK>
 __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 (&qh)[HD / 32],
-                                           const half8 (&ql)[HD / 32], int p0, int tk, int grp,
+                                           const half8 (&ql)[HD / 32], const floatx4 (&qbias)[HD / 32],
+                                           int p0, int tk, int grp,
                                            float score_l2, float& m_run, float& l_run,
                                            floatx4 (&o)[HD / 16]) {
     constexpr int NS = HD / 32;
@@ -274,16 +285,15 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
                 acc = mfma16(f.kh[T][s], ql[s], acc);
                 acc = mfma16(f.kl[T][s], qh[s], acc);
             } else {
+                // K enters biased (1152 + code); the accumulator starts at
+                // -1152 * sum(q over the block's 32 dims), which removes it.
                 const uint4& w = f.kc[T][s >> 1];
-                const half8 kq = (s & 1) ? dq8(w.z, w.w) : dq8(w.x, w.y);
-                floatx4 b = mfma16(kq, qh[s], zero_f4());
+                const half8 kq = (s & 1) ? dq8_biased(w.z, w.w) : dq8_biased(w.x, w.y);
+                floatx4 b = mfma16(kq, qh[s], qbias[s]);
                 b = mfma16(kq, ql[s], b);
-                // Key 8g + 4T + r, dim block s: element (4T + r) * NS + s of the scale run.
+                // Key 8g + 4T + r, dim block s: half 4T + r of the block's scale piece.
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int e = (4 * T + r) * NS + s;
-                    acc[r] += (float)h_at(f.ks[e >> 3], e & 7) * b[r];
-                }
+                for (int r = 0; r < 4; ++r) acc[r] += (float)h_at(f.ks[s], 4 * T + r) * b[r];
             }
         }
 #pragma unroll
@@ -293,7 +303,7 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
     float mx = ninf();
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        sc[j] = (!MASK || kb + j < tk) ? sc[j] * score_l2 : ninf();
+        sc[j] = (!MASK || kb + j < tk) ? sc[j] : ninf();
         mx = fmaxf(mx, sc[j]);
     }
     mx = max4grp(mx);
@@ -307,21 +317,41 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
         ps += p[j];
     }
     l_run = l_run * fac + ps;
+    // Once the running max has settled it rarely moves: skip the rescale of
+    // the context when no lane's factor differs from one.
+    if (__any(fac != 1.0f)) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) o[t] *= fac;
+        for (int t = 0; t < NT; ++t) o[t] *= fac;
+    }
 
     if constexpr (KIND == KV_TQ8) {
         // P' = P * d_v (the scale of each key's dim block) as one f16 operand
-        // per block: Q8_0 values carry 8 bits, so the 11 of an f16 P' keep
-        // the product well inside the quantisation's own error.
+        // per dim block, formed with packed f16 multiplies: Q8_0 values carry
+        // 8 bits, so the 11 of an f16 P' keep the product well inside the
+        // quantisation's own error.
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        h2 ph[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a0 = (!MASK || kb + 2 * i < tk) ? p[2 * i] : 0.0f;
+            const float a1 = (!MASK || kb + 2 * i + 1 < tk) ? p[2 * i + 1] : 0.0f;
+            ph[i] = h2{to_h(a0), to_h(a1)};
+        }
 #pragma unroll
         for (int b = 0; b < NS; ++b) {
+            const uint32_t dw[4] = {f.vs[b].x, f.vs[b].y, f.vs[b].z, f.vs[b].w};
             half8 pv;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int e = j * NS + b;
-                const float d = (float)h_at(f.vs[e >> 3], e & 7);
-                pv[j] = to_h((!MASK || kb + j < tk) ? p[j] * d : 0.0f);
+            for (int i = 0; i < 4; ++i) {
+                h2 d = __builtin_bit_cast(h2, dw[i]);
+                if constexpr (MASK) {
+                    // a tail key's scale may be any bit pattern: zero it too
+                    if (kb + 2 * i >= tk) d[0] = (half_t)0.0f;
+                    if (kb + 2 * i + 1 >= tk) d[1] = (half_t)0.0f;
+                }
+                const h2 x = ph[i] * d;
+                pv[2 * i] = x[0];
+                pv[2 * i + 1] = x[1];
             }
 #pragma unroll
             for (int t = 2 * b; t < 2 * b + 2; ++t) {
@@ -375,6 +405,123 @@ __device__ __forceinline__ void emit(float* out, int8_t* tc, float* ts, size_t i
         const float inv = d > 0.0f ? 1.0f / d : 0.0f;
         tc[idx] = (int8_t)(int)rintf(y * inv);
         if ((threadIdx.x & 31) == 0) ts[idx >> 5] = d;
+    }
+}
+
+// The merge of one head's split partials, in split order, with every load of
+// it issued before any is waited on (one memory round trip), by one
+// workgroup of DT threads. COH: the partials were handed over with coherent
+// stores inside this launch (read them the same way); otherwise a launch
+// boundary separates writer and reader. `lds` holds >= 4096 floats.
+// Thread t owns float4 column c = t % C of the [g][HD] partial (C = n / 4)
+// and the splits s = t / C, t / C + R, ... (R = DT / C phases).
+template <int HD, bool COH>
+__device__ __forceinline__ void merge_head(const float* po, const float* pml, int nsplit, int group, float* lds,
+                                           float* gl, float* out, int8_t* tc, float* ts, size_t obase) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int n = group * HD;
+    const int C = n / 4;
+    const int R = C >= DT ? 1 : DT / C;
+    float* red = lds;          // [R][n] per-phase sums (<= 2048 floats)
+    float* wts = lds + 2048;   // [nsplit][group] weights (<= 1024 floats)
+    // Every load first: this thread's partial columns (up to 16 splits in
+    // flight), then the (m, l) pairs; nothing waits before all are issued.
+    constexpr int U = 16;
+    const int w0 = tid;  // first work item; with C < DT each thread has at most one
+    const int c4 = w0 % C, phase = w0 / C;
+    const bool has = w0 < R * C;
+    float4 x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int sp = phase + u * R;
+        const float* src = po + (size_t)sp * n + 4 * c4;
+        x[u] = (has && sp < nsplit) ? (COH ? ld_coherent4(src) : *reinterpret_cast<const float4*>(src))
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // Weights: for query head g (a wave per g), M_g = max_s m, w_sg = 2^(m - M),
+    // L_g = sum_s l w, reduced across the wave's lanes.
+    for (int g = wave; g < group; g += DW) {
+        float mv[4], lv[4];
+        float mx = ninf();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int sp = lane + 64 * k;
+            const float* src = pml + ((size_t)sp * group + g) * 2;
+            mv[k] = sp < nsplit ? (COH ? ld_coherent(src) : src[0]) : ninf();
+            lv[k] = sp < nsplit ? (COH ? ld_coherent(src + 1) : src[1]) : 0.0f;
+            mx = fmaxf(mx, mv[k]);
+        }
+#pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int sp = lane + 64 * k;
+            if (sp < nsplit) {
+                const float w = ex2(mv[k] - mx);
+                wts[sp * group + g] = w;
+                L += lv[k] * w;
+            }
+        }
+#pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) L += __shfl_xor(L, o2, 64);
+        if (lane == 0) gl[g] = L;
+    }
+    __syncthreads();
+    if (has) {
+        const int g = (4 * c4) / HD;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int sp = phase + u * R;
+            const float wt = sp < nsplit ? wts[sp * group + g] : 0.0f;
+            acc.x += x[u].x * wt;
+            acc.y += x[u].y * wt;
+            acc.z += x[u].z * wt;
+            acc.w += x[u].w * wt;
+        }
+        // Splits beyond the first U * R (long contexts): more rounds.
+        for (int s0 = phase + U * R; s0 < nsplit; s0 += U * R) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int sp = s0 + u * R;
+                const float* src = po + (size_t)sp * n + 4 * c4;
+                x[u] = sp < nsplit ? (COH ? ld_coherent4(src) : *reinterpret_cast<const float4*>(src))
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int sp = s0 + u * R;
+                const float wt = sp < nsplit ? wts[sp * group + g] : 0.0f;
+                acc.x += x[u].x * wt;
+                acc.y += x[u].y * wt;
+                acc.z += x[u].z * wt;
+                acc.w += x[u].w * wt;
+            }
+        }
+        reinterpret_cast<float4*>(red + phase * n)[c4] = acc;
+    }
+    // Columns beyond DT (C > DT): the remaining work items, one round each.
+    for (int w = w0 + DT; w < C; w += DT) {
+        const int g = (4 * w) / HD;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int sp = 0; sp < nsplit; ++sp) {
+            const float* src = po + (size_t)sp * n + 4 * w;
+            const float4 y = COH ? ld_coherent4(src) : *reinterpret_cast<const float4*>(src);
+            const float wt = wts[sp * group + g];
+            acc.x += y.x * wt;
+            acc.y += y.y * wt;
+            acc.z += y.z * wt;
+            acc.w += y.w * wt;
+        }
+        reinterpret_cast<float4*>(red)[w] = acc;
+    }
+    __syncthreads();
+    for (int e = tid; e < n; e += DT) {
+        float acc = 0.0f;
+        for (int r = 0; r < R; ++r) acc += red[r * n + e];
+        emit(out, tc, ts, obase + e, acc / gl[e / HD]);
     }
 }
 
@@ -434,7 +581,9 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     if (nf > 0) load_block<HD, KIND, VA, true>(c, first * 32, lane, f0);
 
     // The group's queries as B operands, hi + lo (columns past the group are
-    // read from column 0 and zeroed, so every load is unconditional).
+    // read from column 0 and zeroed, so every load is unconditional). The
+    // score scale and log2(e) ride on the query, so a product is already a
+    // log2-unit score.
     const float* q = a.q + a.q_off + (size_t)seq * a.q_stride + ((size_t)h * group) * HD;
     const bool qok = col < group;
     const float* qc = q + (size_t)(qok ? col : 0) * HD + 8 * grp;
@@ -452,10 +601,24 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             half_t hh, ll;
-            split_h(qok ? x[j] * a.qscale : 0.0f, hh, ll);
+            split_h(qok ? x[j] * a.qscale * a.score_l2 : 0.0f, hh, ll);
             qh[s][j] = hh;
             ql[s][j] = ll;
         }
+    }
+
+    // -1152 * (the block-s dims of q summed), per query column: the
+    // accumulator start that cancels the offset of biased Q8_0 K codes.
+    floatx4 qbias[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        float t = 0.0f;
+        if constexpr (KIND == KV_TQ8) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t += (float)qh[s][j] + (float)ql[s][j];
+            t = -1152.0f * sum4grp(t);
+        }
+        qbias[s] = floatx4{t, t, t, t};
     }
 
     float m_run = ninf(), l_run = 0.0f;
@@ -463,19 +626,28 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
 #pragma unroll
     for (int t = 0; t < NT; ++t) o[t] = zero_f4();
 
-    int i = 0;
-    for (; i + 1 < nf; i += 2) {
+    // Every prefetch is unconditional (a block past this wave's last is
+    // clamped to its last and simply re-read): the wait counter then stands
+    // at the same count on every path into a fold, so each fold waits only
+    // for its own block. The scheduling barriers keep each prefetch ahead of
+    // the fold it is meant to overlap (left alone, the scheduler sinks loads
+    // towards their uses).
+    for (int i = 0; i < nf; i += 2) {
         const int p0 = (first + i * DW) * 32;
-        const int p1 = p0 + DW * 32;
+        const int p1 = (first + min(i + 1, nf - 1) * DW) * 32;
+        const int p2 = (first + min(i + 2, nf - 1) * DW) * 32;
         load_block<HD, KIND, VA, true>(c, p1, lane, f1);
-        fold_block<HD, KIND, false>(f0, qh, ql, p0, tk, grp, a.score_l2, m_run, l_run, o);
-        if (i + 2 < nf) load_block<HD, KIND, VA, true>(c, p1 + DW * 32, lane, f0);
-        fold_block<HD, KIND, false>(f1, qh, ql, p1, tk, grp, a.score_l2, m_run, l_run, o);
+        __builtin_amdgcn_sched_barrier(0);
+        fold_block<HD, KIND, false>(f0, qh, ql, qbias, p0, tk, grp, a.score_l2, m_run, l_run, o);
+        __builtin_amdgcn_sched_barrier(0);
+        load_block<HD, KIND, VA, true>(c, p2, lane, f0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < nf) fold_block<HD, KIND, false>(f1, qh, ql, qbias, p1, tk, grp, a.score_l2, m_run, l_run, o);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    if (i < nf) fold_block<HD, KIND, false>(f0, qh, ql, (first + i * DW) * 32, tk, grp, a.score_l2, m_run, l_run, o);
     if (tail) {
         load_block<HD, KIND, VA, TILED>(c, nfull * 32, lane, f0);
-        fold_block<HD, KIND, true>(f0, qh, ql, nfull * 32, tk, grp, a.score_l2, m_run, l_run, o);
+        fold_block<HD, KIND, true>(f0, qh, ql, qbias, nfull * 32, tk, grp, a.score_l2, m_run, l_run, o);
     }
     l_run = sum4grp(l_run);
 
@@ -531,6 +703,21 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const size_t head = (size_t)seq * gridDim.y + h;
     float* po = a.part + (head * a.splits) * n;
     float* pml = a.part + a.ml_off + (head * a.splits) * group * 2;
+    if (a.two_phase) {
+        // A separate merge launch follows: plain stores, and done.
+        for (int e = tid; e < n; e += DT) {
+            const int g = e / HD, d = e % HD;
+            float acc = 0.0f;
+#pragma unroll
+            for (int w = 0; w < DW; ++w) acc += lds[w * OBS + d * 17 + g];
+            po[(size_t)split * n + e] = acc;
+        }
+        if (tid < group) {
+            pml[((size_t)split * group + tid) * 2] = gm[tid];
+            pml[((size_t)split * group + tid) * 2 + 1] = gl[tid];
+        }
+        return;
+    }
     // Cross-workgroup hand-off without cache-wide fences: the partial is
     // stored with agent-scope (coherent) stores, the stores are waited for,
     // and only then is the arrival counted; the last arriver reads the
@@ -558,64 +745,37 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     __syncthreads();
     if (!last) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-
-    // The merge, in split order, with every load of it issued before any is
-    // waited on: one memory round trip. Thread t owns float4 column
-    // c = t % C of the [g][HD] partial (C = n / 4) and the splits
-    // s = t / C, t / C + R, ... (R = DT / C phases).
-    const int C = n / 4;
-    const int R = C >= DT ? 1 : DT / C;
-    float* red = lds;          // [R][n] per-phase sums (<= 2048 floats)
-    float* wts = lds + 2048;   // [nsplit][group] m then weights, [nsplit][group] l (<= 2048 floats)
-    // Weights: M_g = max_s m, w_sg = 2^(m_sg - M_g), L_g = sum_s l_sg w_sg.
-    for (int i = tid; i < nsplit * group; i += DT) {
-        wts[i] = ld_coherent(pml + 2 * i);
-        wts[nsplit * group + i] = ld_coherent(pml + 2 * i + 1);
-    }
-    __syncthreads();
-    if (tid < group) {
-        float mx = ninf();
-        for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, wts[s * group + tid]);
-        float L = 0.0f;
-        for (int s = 0; s < nsplit; ++s) {
-            const float w = ex2(wts[s * group + tid] - mx);
-            wts[s * group + tid] = w;
-            L += wts[nsplit * group + s * group + tid] * w;
-        }
-        gl[tid] = L;
-    }
-    __syncthreads();
-    for (int w = tid; w < R * C; w += DT) {
-        const int c4 = w % C, phase = w / C;
-        const int g = (4 * c4) / HD;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        constexpr int U = 16;
-        for (int s0 = phase; s0 < nsplit; s0 += U * R) {
-            float4 x[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int s = s0 + u * R;
-                x[u] = s < nsplit ? ld_coherent4(po + (size_t)s * n + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int s = s0 + u * R;
-                const float wt = s < nsplit ? wts[s * group + g] : 0.0f;
-                acc.x += x[u].x * wt;
-                acc.y += x[u].y * wt;
-                acc.z += x[u].z * wt;
-                acc.w += x[u].w * wt;
-            }
-        }
-        reinterpret_cast<float4*>(red + phase * n)[c4] = acc;
-    }
-    __syncthreads();
-    for (int e = tid; e < n; e += DT) {
-        float acc = 0.0f;
-        for (int r = 0; r < R; ++r) acc += red[r * n + e];
-        emit(out, tc, ts, (size_t)h * group * HD + e, acc / gl[e / HD]);
-    }
+    merge_head<HD, true>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The merge of one head's splits as a launch of its own, after a two-phase
+// attention launch: one workgroup per (sequence, kv head).
+template <int HD>
+__global__ __launch_bounds__(DT) void attn_merge_kernel(DecodeArgs a) {
+    __shared__ float lds[4096];
+    __shared__ float gl[16];
+    const int h = blockIdx.x, seq = blockIdx.y;
+    const int group = a.group;
+    const int tk = a.tk_arr ? min(a.tk_arr[seq], a.tk) : a.tk;
+    const int slot = a.slot_arr ? a.slot_arr[seq] : 0;
+    if (a.slot_arr && (slot < 0 || slot >= a.slots || tk <= 0)) return;
+    const int span = DW * a.nit * 32;
+    const int nsplit = (tk + span - 1) / span;
+    if (nsplit <= 1) return;  // the attention launch wrote this head itself
+    const int n = group * HD;
+    const size_t head = (size_t)seq * gridDim.x + h;
+    const float* po = a.part + (head * a.splits) * n;
+    const float* pml = a.part + a.ml_off + (head * a.splits) * group * 2;
+    float* out = a.out + a.out_off + (size_t)seq * a.out_stride;
+    int8_t* tc = nullptr;
+    float* ts = nullptr;
+    if (a.twin_codes) {
+        const size_t oo = a.out_off + (size_t)seq * a.out_stride;
+        tc = a.twin_codes + oo;
+        ts = a.twin_scales + (oo >> 5);
+    }
+    merge_head<HD, false>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
 }
 
 #define DECODE_INST(HD, KIND, VA) template __global__ void attn_decode_kernel<HD, KIND, VA>(DecodeArgs);
@@ -623,7 +783,17 @@ DECODE_INST(64, KV_F16, 16) DECODE_INST(128, KV_F16, 16) DECODE_INST(64, KV_F16,
 DECODE_INST(64, KV_F32, 16) DECODE_INST(128, KV_F32, 16) DECODE_INST(64, KV_F32, 8) DECODE_INST(128, KV_F32, 8)
 DECODE_INST(64, KV_T16, 16) DECODE_INST(128, KV_T16, 16) DECODE_INST(64, KV_TQ8, 16) DECODE_INST(128, KV_TQ8, 16)
 
-hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
+template __global__ void attn_merge_kernel<64>(DecodeArgs);
+template __global__ void attn_merge_kernel<128>(DecodeArgs);
+
+static hipError_t launch_merge(int hd, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
+    dim3 grid(kv_heads, nseq), block(DT);
+    if (hd == 64) hipLaunchKernelGGL((attn_merge_kernel<64>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((attn_merge_kernel<128>), grid, block, 0, st, a);
+    return hipGetLastError();
+}
+
+static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
     dim3 grid(a.splits, kv_heads, nseq), block(DT);
     const int esz = kind == KV_F32 ? 4 : 2;
     const int va = (kind == KV_T16 || kind == KV_TQ8) ? 16 : (((long)a.cap * esz) % 16 == 0 ? 16 : 8);
@@ -637,6 +807,12 @@ hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, in
     L(64, KV_T16, 16) L(128, KV_T16, 16) L(64, KV_TQ8, 16) L(128, KV_TQ8, 16)
 #undef L
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
+    hipError_t e = launch_attn(hd, kind, a, kv_heads, nseq, st);
+    if (e != hipSuccess || !a.two_phase || a.splits <= 1) return e;
+    return launch_merge(hd, a, kv_heads, nseq, st);
 }
 
 }  // namespace llmtie

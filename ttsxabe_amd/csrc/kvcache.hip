@@ -130,7 +130,7 @@ __device__ __forceinline__ Q8At q8_at(size_t kvh, int nblk, int hd, int p, int d
     const int kk = p & 31;
     Q8At r;
     r.code = blk + (value ? 32L * hd + tq8_v_off(kk, d) : tq8_k_off(hd, kk, d));
-    r.scale = blk + 64L * hd + (value ? 64L * (hd / 32) : 0) + 2L * (kk * (hd / 32) + (d >> 5));
+    r.scale = blk + 64L * hd + (value ? 64L * (hd / 32) : 0) + 2L * ((d >> 5) * 32 + kk);
     return r;
 }
 
@@ -156,13 +156,13 @@ __global__ __launch_bounds__(KB) void append_q8_kernel(const float* k, long k_of
     q8_block(live ? k[k_off + ii] : 0.0f, c, db);
     if (live) {
         const Q8At at = q8_at(kvh, nb, hd, past + ti, j, false);
-        cache[at.code] = c;
+        cache[at.code] = (char)(c ^ 0x80);
         if ((j & 31) == 0) *reinterpret_cast<uint16_t*>(cache + at.scale) = db;
     }
     q8_block(live ? v[v_off + ii] : 0.0f, c, db);
     if (live) {
         const Q8At at = q8_at(kvh, nb, hd, past + ti, j, true);
-        cache[at.code] = c;
+        cache[at.code] = (char)(c ^ 0x80);
         if ((j & 31) == 0) *reinterpret_cast<uint16_t*>(cache + at.scale) = db;
     }
 }
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(KB) void rope_cache_q8_kernel(float* q, long q_off,
     q8_block(x, c, db);
     if (!live) return;
     const Q8At at = q8_at((size_t)slot * kv + hh, tiled_nblk(cap), hd, pos, jj, !is_k);
-    cache[at.code] = c;
+    cache[at.code] = (char)(c ^ 0x80);
     if ((jj & 31) == 0) *reinterpret_cast<uint16_t*>(cache + at.scale) = db;
 }
 

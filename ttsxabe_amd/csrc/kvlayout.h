@@ -15,12 +15,15 @@
 //   A head's blocks are contiguous: block b of kv head h at (h*nblk + b) * 64*HD halves.
 //
 // Q8_0 tiled block (GGUF Q8_0: 32 int8 codes share one f16 scale d, value
-// d * code; the 32 codes of a scale are 32 consecutive dims of one position):
+// d * code; the 32 codes of a scale are 32 consecutive dims of one position).
+// Codes are stored offset-binary (code + 128 as an unsigned byte, i.e. the
+// sign bit flipped), the form the kernel splices straight into f16 bits:
 //   K codes, 32*HD bytes: ((T*(NS/2) + s/2)*64 + l)*16 + 8*(s%2) + j  holds
 //       key 8*(col/4) + 4T + col%4, dim 32s + 8g + j
 //   V codes, 32*HD bytes: ((t/2)*64 + l)*16 + 8*(t%2) + j  holds  dim 16t + col, key 8g + j
-//   K scales, 32*(HD/32) halves: key-major, [key][dim block]
-//   V scales, the same.
+//   K scales, 32*(HD/32) halves: [dim block][key]
+//   V scales, the same (so the scales of 8 consecutive keys for one dim block
+//   are one 16-byte read, and pair up with packed f16 probabilities).
 //   Block bytes: 2*32*HD + 2*32*(HD/32)*2 (8704 at HD 128 = 272 per position).
 //   Block b of (slot, kv head h) at ((slot*kv + h)*nblk + b) * block bytes.
 #pragma once

@@ -170,6 +170,9 @@ class KvCacheQ8:
         self.slots, self.kv_heads, self.head_dim, self.cap = slots, kv_heads, head_dim, cap
         n = _lib.lib().llmtie_q8_cache_bytes(slots, kv_heads, head_dim, cap)
         self.data = torch.zeros(n, dtype=torch.int8, device=device)
+        # An empty cache holds code 0 (offset-binary 0x80) with scale 0.
+        blocks = self.data.view(-1, n // (slots * kv_heads * ((cap + 31) // 32)))
+        blocks[:, : 64 * head_dim].fill_(-128)
 
     def bytes_per_position(self) -> int:
         """HBM bytes one live position of one sequence costs a decode step."""
