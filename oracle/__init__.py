@@ -10,7 +10,7 @@ Pinning status of each function (see tests/test_oracle.py):
   f32_to_f16 / f16_to_f32   pinned: numpy float16 (IEEE RNE) on all 2^16 halves
                             and on edge/tie/subnormal f32 inputs
   seq                       pinned: reference's own xorshift recurrence run in
-                            Python big ints; range [-2, 2]
+                            Python big ints (tests/golden); range [-2, 6)
   normal                    pinned: moments and KS statistic (generator only)
   rope                      pinned: complex-rotation closed form in f64,
                             position 0 identity, pair-norm preservation

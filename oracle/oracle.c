@@ -84,7 +84,8 @@ static double h16(float x) { return (double)orc_f16_to_f32(orc_f32_to_f16(x)); }
 
 /* ---------------------------------------------------------- generators */
 
-/* The reference tests' deterministic spread in [-2, 2]: xorshift64 with
+/* The reference tests' deterministic spread, uniform on [-2, 6) (the doc
+ * comment there says "roughly [-2, 2]"; the formula is what counts): xorshift64 with
  * shifts 13, 7, 17 seeded from salt * golden ratio | 1
  * (crates/llmtie-cuda/tests/kernels.rs:35-46). */
 void orc_seq(float* out, size_t n, uint64_t salt) {
