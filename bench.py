@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB a few times (the known-size kernel that "
+                         "calibrates the FETCH_SIZE / WRITE_SIZE counters) and exit")
     return ap.parse_args()
 
 
@@ -284,6 +287,15 @@ def main():
                                    "shards by head/sequence with no exchange, see DESIGN.md"}))
         sys.exit(2)
     import torch
+    if a.copy_calibration:
+        n = a.copy_calibration * 2 ** 20 // 2
+        src = torch.ones(n, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 2 * n, "launches": 5}), flush=True)
+        return
     from ttsxabe_amd.gpu import Gpu
     g = Gpu(0)
     print("bench: C2 decode", file=sys.stderr, flush=True)
@@ -308,7 +320,7 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(c2["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(c2["frac"], 4), "traffic": traffic_from_profiles("attn_decode_c2_counters.md"),
-                     "kernel": "attn_decode_kernel<128, KV_T16> (+ attn_merge_kernel)",
+                     "kernel": "attn_decode_kernel<128, KV_T16> (split merge by the last-arriving workgroup, one kernel per launch)",
                      "bytes_per_launch": c2["bytes_per_launch"],
                      "us_per_launch": round(c2["us_per_launch"], 3)},
     }

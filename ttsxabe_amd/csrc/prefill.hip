@@ -124,35 +124,32 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
 
     // Tiled cache: a 64-key tile is two blocks; each block's K and V areas are
     // copied verbatim (16-byte chunk i of an area to LDS chunk i), so the
-    // fragment reads below are lane-contiguous and conflict-free. V chunks of
-    // keys >= ktot are zeroed (a tiled cache holds garbage there).
+    // fragment reads below are lane-contiguous and conflict-free. The loads
+    // are unconditional, from the block clamped to the last one holding a key
+    // below kend, so they pipeline without branches; keys past the live ones
+    // are handled after the data has arrived (store_tile): their scores are
+    // masked to -inf, and their V chunks are zeroed there, since a tiled
+    // cache may hold non-finite garbage past ktot and 0 * NaN is NaN.
     const size_t tblk = (size_t)kh * tiled_nblk(a.cap);  // first block of this kv head
+    const int lastb = (max(kend, 1) - 1) >> 5;            // last block with a key below kend
     auto load_tile = [&](int kv0, St& st) {
         if constexpr (KIND == PF_T16) {
             constexpr int AREA = 32 * HD / 8;  // 16-byte chunks per area
+            static_assert(PT % AREA == 0 || AREA % PT == 0, "a chunk's block index must be wave-uniform");
+            const half8* base = reinterpret_cast<const half8*>(a.k) + tblk * (2 * AREA);
 #pragma unroll
             for (int i = 0; i < St::KC; ++i) {
                 const int id = tid + PT * i;       // 0 .. 2*AREA-1 over the two blocks
                 const int hb = id / AREA, ci = id % AREA;
-                const int b0 = kv0 + 32 * hb;
-                const half8* src = reinterpret_cast<const half8*>(a.k) + (tblk + (b0 >> 5)) * (2 * AREA);
-                st.k[i] = b0 < ktot ? src[ci] : zero_h8();
+                const int b = min((kv0 >> 5) + hb, lastb);
+                st.k[i] = base[(size_t)b * (2 * AREA) + ci];
             }
 #pragma unroll
             for (int i = 0; i < St::VC; ++i) {
                 const int id = tid + PT * i;
                 const int hb = id / AREA, ci = id % AREA;
-                const int b0 = kv0 + 32 * hb;
-                const half8* src = reinterpret_cast<const half8*>(a.k) + (tblk + (b0 >> 5)) * (2 * AREA) + AREA;
-                half8 x = zero_h8();
-                if (b0 < ktot) {
-                    x = src[ci];
-                    const int k0 = b0 + 8 * ((ci & 63) >> 4);  // keys of this chunk: k0 .. k0 + 7
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        if (k0 + j >= ktot) x[j] = (half_t)0.0f;
-                }
-                st.v[i] = x;
+                const int b = min((kv0 >> 5) + hb, lastb);
+                st.v[i] = base[(size_t)b * (2 * AREA) + AREA + ci];
             }
         } else {
 #pragma unroll
@@ -176,7 +173,7 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
             }
         }
     };
-    auto store_tile = [&](const St& st) {
+    auto store_tile = [&](int kv0, const St& st) {
         if constexpr (KIND == PF_T16) {
             constexpr int AREA = 32 * HD / 8;
 #pragma unroll
@@ -187,9 +184,16 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < St::VC; ++i) {
                 const int id = tid + PT * i;
-                reinterpret_cast<half8*>(vs)[id] = st.v[i];
+                half8 x = st.v[i];
+                const int b0 = kv0 + 32 * (id / AREA);  // uniform: AREA is a multiple of the wave
+                if (b0 + 32 > ktot) {                   // the tail block, or one wholly past ktot
+                    const int k0 = b0 + 8 * (((id % AREA) & 63) >> 4);  // keys k0 .. k0 + 7
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if (k0 + j >= ktot) x[j] = (half_t)0.0f;
+                }
+                reinterpret_cast<half8*>(vs)[id] = x;
             }
-            (void)AREA;
             return;
         }
 #pragma unroll
@@ -270,7 +274,7 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
     if (kend > 0) load_tile(0, st);
     for (int kv0 = 0; kv0 < kend; kv0 += KT) {
         __syncthreads();  // previous tile fully consumed
-        store_tile(st);
+        store_tile(kv0, st);
         __syncthreads();
         if (kv0 + KT < kend) load_tile(kv0 + KT, st);
         if (kv0 > wlim) continue;
