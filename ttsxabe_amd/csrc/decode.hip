@@ -408,11 +408,13 @@ __device__ __forceinline__ void emit(float* out, int8_t* tc, float* ts, size_t i
     }
 }
 
-// The merge of one head's split partials, in split order, with every load of
-// it issued before any is waited on (one memory round trip), by one
-// workgroup of DT threads. COH: the partials were handed over with coherent
-// stores inside this launch (read them the same way); otherwise a launch
-// boundary separates writer and reader. `lds` holds >= 4096 floats.
+// The merge of one head's split partials, in split order, by one workgroup
+// of DT threads, with every load issued before any is waited on (one memory
+// round trip): first the (m, l) pairs the weights need, then the partial
+// columns, so the weights are computed while the columns are in flight.
+// COH: the partials were handed over with coherent stores inside this launch
+// (read them with the same agent-scope policy); otherwise a launch boundary
+// separates writer and reader. `lds` holds >= 4096 floats.
 // Thread t owns float4 column c = t % C of the [g][HD] partial (C = n / 4)
 // and the splits s = t / C, t / C + R, ... (R = DT / C phases).
 template <int HD, bool COH>
@@ -425,43 +427,51 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
     const int R = C >= DT ? 1 : DT / C;
     float* red = lds;          // [R][n] per-phase sums (<= 2048 floats)
     float* wts = lds + 2048;   // [nsplit][group] weights (<= 1024 floats)
-    // Every load first: this thread's partial columns (up to 16 splits in
-    // flight), then the (m, l) pairs; nothing waits before all are issued.
+    const Region ro = region(po, (uint32_t)((size_t)nsplit * n * 4));
+    const Region rml = region(pml, (uint32_t)((size_t)nsplit * group * 8));
+
+    // (m, l) of query head g0 = wave for splits lane + 64k.
+    constexpr int MK = DECODE_MAX_SPLITS / 64;
+    float2 ml[MK];
+    const int g0 = wave;
+#pragma unroll
+    for (int k = 0; k < MK; ++k) {
+        ml[k] = make_float2(0.f, 0.f);
+        if (64 * k < nsplit && g0 < group) ml[k] = ld_region2<COH>(rml, (uint32_t)(((lane + 64 * k) * group + g0) * 8));
+    }
+    // This thread's partial columns, up to U splits in flight.
     constexpr int U = 16;
-    const int w0 = tid;  // first work item; with C < DT each thread has at most one
-    const int c4 = w0 % C, phase = w0 / C;
-    const bool has = w0 < R * C;
+    const int c4 = tid % C, phase = tid / C;
+    const bool has = tid < R * C;
     float4 x[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int sp = phase + u * R;
-        const float* src = po + (size_t)sp * n + 4 * c4;
-        x[u] = (has && sp < nsplit) ? (COH ? ld_coherent4(src) : *reinterpret_cast<const float4*>(src))
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+        x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (has && u * R < nsplit) x[u] = ld_region4<COH>(ro, (uint32_t)(((size_t)sp * n + 4 * c4) * 4));
     }
     // Weights: for query head g (a wave per g), M_g = max_s m, w_sg = 2^(m - M),
     // L_g = sum_s l w, reduced across the wave's lanes.
     for (int g = wave; g < group; g += DW) {
-        float mv[4], lv[4];
+        if (g != g0) {
+#pragma unroll
+            for (int k = 0; k < MK; ++k)
+                if (64 * k < nsplit) ml[k] = ld_region2<COH>(rml, (uint32_t)(((lane + 64 * k) * group + g) * 8));
+        }
         float mx = ninf();
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int sp = lane + 64 * k;
-            const float* src = pml + ((size_t)sp * group + g) * 2;
-            mv[k] = sp < nsplit ? (COH ? ld_coherent(src) : src[0]) : ninf();
-            lv[k] = sp < nsplit ? (COH ? ld_coherent(src + 1) : src[1]) : 0.0f;
-            mx = fmaxf(mx, mv[k]);
-        }
+        for (int k = 0; k < MK; ++k)
+            if (lane + 64 * k < nsplit) mx = fmaxf(mx, ml[k].x);
 #pragma unroll
         for (int o2 = 32; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
         float L = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < MK; ++k) {
             const int sp = lane + 64 * k;
             if (sp < nsplit) {
-                const float w = ex2(mv[k] - mx);
+                const float w = ex2(ml[k].x - mx);
                 wts[sp * group + g] = w;
-                L += lv[k] * w;
+                L += ml[k].y * w;
             }
         }
 #pragma unroll
@@ -484,12 +494,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
         // Splits beyond the first U * R (long contexts): more rounds.
         for (int s0 = phase + U * R; s0 < nsplit; s0 += U * R) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int sp = s0 + u * R;
-                const float* src = po + (size_t)sp * n + 4 * c4;
-                x[u] = sp < nsplit ? (COH ? ld_coherent4(src) : *reinterpret_cast<const float4*>(src))
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            for (int u = 0; u < U; ++u) x[u] = ld_region4<COH>(ro, (uint32_t)(((size_t)(s0 + u * R) * n + 4 * c4) * 4));
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int sp = s0 + u * R;
@@ -503,12 +508,11 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
         reinterpret_cast<float4*>(red + phase * n)[c4] = acc;
     }
     // Columns beyond DT (C > DT): the remaining work items, one round each.
-    for (int w = w0 + DT; w < C; w += DT) {
+    for (int w = tid + DT; w < C; w += DT) {
         const int g = (4 * w) / HD;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int sp = 0; sp < nsplit; ++sp) {
-            const float* src = po + (size_t)sp * n + 4 * w;
-            const float4 y = COH ? ld_coherent4(src) : *reinterpret_cast<const float4*>(src);
+            const float4 y = ld_region4<COH>(ro, (uint32_t)(((size_t)sp * n + 4 * w) * 4));
             const float wt = wts[sp * group + g];
             acc.x += y.x * wt;
             acc.y += y.y * wt;
