@@ -35,11 +35,15 @@ def hipcc() -> str:
     return cand
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into the in-tree shared library."""
-    srcs = [str(CSRC / s) for s in SOURCES]
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, "-I", str(ROOT / "include"), *srcs, "-o", str(tmp)]
+# Per-source extra flags. The prefill kernels' softmax takes maxima of raw
+# MFMA outputs; with NaNs honoured every fmaxf operand first gets a
+# canonicalising v_max of its own. Infinities (the -inf of masked keys)
+# stay honoured.
+EXTRA = {"prefill.hip": ["-fno-honor-nans"]}
+COMPILE = [f for f in FLAGS if f != "-shared"]
+
+
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -49,6 +53,22 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source (one object each, in parallel) and link the
+    in-tree shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+    out = PKG / "_build"
+    out.mkdir(exist_ok=True)
+    objs = [out / (Path(s).stem + ".o") for s in SOURCES]
+    cmds = [[hipcc(), *COMPILE, *EXTRA.get(s, []), "-I", str(ROOT / "include"), "-c", str(CSRC / s), "-o", str(o)]
+            for s, o in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(len(cmds)) as ex:
+        for f in [ex.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([hipcc(), *FLAGS, *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB)
     return LIB
 

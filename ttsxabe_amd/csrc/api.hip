@@ -113,12 +113,12 @@ int pick_nqt(size_t tq, size_t heads, int gb) {
         const int v = atoi(e);
         if (v == 1 || v == 2 || v == 4) return v;
     }
-    const int cands[3] = {4, 2, 1};
-    for (int nqt : cands) {
-        const size_t pb = 16 * nqt * (4 / gb);
-        const size_t wgs = ((tq + pb - 1) / pb) * (heads / gb);
-        if (wgs >= 512) return nqt;
-    }
+    // Measured on MI355X (C3 shapes, 512 to 8192 rows): two 16-row query
+    // tiles per wave (each K/V fragment read from LDS feeds two MFMAs) win
+    // once the launch still has >= 512 workgroups; below that, one tile per
+    // wave, for the parallelism.
+    const size_t pb2 = 32 * (4 / gb);
+    if (((tq + pb2 - 1) / pb2) * (heads / gb) >= 512) return 2;
     return 1;
 }
 
@@ -136,7 +136,7 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
     if (!q || !k || !v || !out) return invalid("a buffer");
     const size_t group = heads / kv_heads;
     const int gb = group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
-    PrefillArgs a;
+    PrefillArgs a{};
     a.q = q;
     a.k = k;
     a.v = v;
@@ -153,6 +153,7 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
     a.kvs = 0;
     a.os = (int)(heads * hd);
     a.scale_q = 0;
+    a.v_bytes = v_len * (kind == PF_F32 ? 4 : 2);
     return launched("flash_attn", launch_prefill((int)hd, kind, pick_nqt(tq, heads, gb), a, S(stream)));
 }
 
@@ -324,7 +325,7 @@ int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint1
     if (out_len < t * d) return overrun_slice(t * d, out_len);
     if (t == 0) return ok();
     if (!qkv || !out) return invalid("a buffer");
-    PrefillArgs a;
+    PrefillArgs a{};
     a.q = qkv;
     a.k = qkv + d;
     a.v = qkv + 2 * d;

@@ -90,16 +90,24 @@ __device__ __forceinline__ half8 ld_q8x8(const int8_t* p) {
     return r;
 }
 
-// Cross-lane reductions over the four lanes that share `col` (xor 16, 32).
+// Cross-lane reductions over the four lanes that share `col` (xor 16, 32),
+// on the VALU rather than through the LDS crossbar. v_permlane16_swap with
+// both operands = v exchanges the odd 16-lane row of each row pair with the
+// even one, so afterwards the two results hold, in every lane of the pair,
+// the even row's v and the odd row's v; v_permlane32_swap does the same for
+// the two 32-lane halves. Combining the two results is then the pairwise
+// step of the reduction (commutative, so every lane gets identical bits).
 __device__ __forceinline__ float max4grp(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float sum4grp(float v) {
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Agent-scope (device-coherent) 32-bit store and loads: visible across the

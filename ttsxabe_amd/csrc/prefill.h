@@ -26,6 +26,7 @@ struct PrefillArgs {
     int kvs;          // PF_ROWS: k/v row stride, elements
     int os;           // out row stride, elements
     int scale_q;      // the scale goes on q before rounding (else on the scores)
+    size_t v_bytes;   // PF_F16: bytes of the V cache allocation (bounds the tile loads)
 };
 
 // nqt: 16-query tiles per wave (1, 2 or 4).

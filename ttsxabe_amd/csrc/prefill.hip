@@ -28,6 +28,8 @@
 //
 // LDS rows are XOR-swizzled by 16-byte chunk so that the eight rows one
 // ds_read_b128 phase touches land on distinct banks.
+#include <stdlib.h>
+#include <type_traits>
 #include "common.h"
 #include "prefill.h"
 #include "kvlayout.h"
@@ -371,6 +373,280 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
     }
 }
 
+
+// ------------------------------------------------------------------------
+// The f16-cache fast path (PF_F16 and PF_T16). Same work decomposition and
+// arithmetic as flash_prefill_kernel, with the K/V tiles moved straight from
+// global memory into LDS by global_load_lds_dwordx4 / buffer_load ... lds
+// (no staging registers, no LDS store instructions), double-buffered with
+// one barrier per tile, and the causal/tail mask applied only to the tiles
+// that need it.
+//
+// LDS tile = the 64 keys' K fragments then V fragments, each fragment 64
+// lanes x 16 bytes in exactly the order the MFMA A-operand reads take them
+// (the tiled cache's fragment order): K fragment (half, T, s) holds, in lane
+// l, key 32*half + 8*(col/4) + 4T + col%4, dims 32s + 8grp .. +7; V fragment
+// (half, t) holds dim 16t + col, keys 32*half + 8grp .. +7. A tiled-cache
+// tile is therefore two blocks copied verbatim; a reference-layout tile is
+// gathered by giving each lane the global address of its chunk. Reads are
+// lane-contiguous and conflict-free either way.
+//
+// Keys past the cache's live ones: K rows are clamped to the last live row
+// (their scores are masked); V chunks past ktot may hold anything, so in the
+// one tile that reaches past ktot they are zeroed in LDS before use.
+template <int HD, int KIND, int NQT>
+__global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
+    static_assert(KIND == PF_F16 || KIND == PF_T16, "f16 caches only");
+    constexpr int NS = HD / 32;
+    constexpr int NT = HD / 16;
+    constexpr int QPW = 16 * NQT;
+    constexpr int KF = 4 * NS;          // K fragments per tile
+    constexpr int VF = 2 * NT;          // V fragments per tile
+    constexpr int FH = 64 * 8;          // halves per fragment
+    constexpr int NF = (KF + VF) / PW;  // fragments each wave loads per tile
+    static_assert((KF + VF) % PW == 0, "fragments split evenly over the waves");
+    __shared__ __attribute__((aligned(16))) half_t t0[(KF + VF) * FH];
+    __shared__ __attribute__((aligned(16))) half_t t1[(KF + VF) * FH];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int gb = a.gb;
+    const int pb = QPW * (PW / gb);
+    const int group = a.heads / a.kv_heads;
+    const int bx = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int h = blockIdx.y * gb + wave % gb;
+    const int kh = (blockIdx.y * gb) / group;
+    const int bp0 = bx * pb;
+    const int p0 = bp0 + (wave / gb) * QPW;
+    const int ktot = a.past + a.tq;
+    const int kend = a.causal ? min(ktot, a.past + bp0 + pb) : ktot;
+    // The last key any row of this wave sees, and the last key all of them see.
+    const int wlim = a.causal ? min(a.past + p0 + QPW - 1, ktot - 1) : ktot - 1;
+    const int wall = a.causal ? min(a.past + p0, ktot - 1) : ktot - 1;
+
+    const half_t* kc = static_cast<const half_t*>(a.k);
+    const size_t tblk = (size_t)kh * tiled_nblk(a.cap);
+    const int lastb = (max(kend, 1) - 1) >> 5;
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.v), 0, (int)(uint32_t)a.v_bytes, 0x00020000);
+
+    auto issue = [&](int kv0, half_t* dst) {
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            const int f = wave + PW * i;
+            half_t* l = dst + f * FH;
+            if constexpr (KIND == PF_T16) {
+                const int hf = f < KF ? f / (2 * NS) : (f - KF) / NT;
+                const int b = min((kv0 >> 5) + hf, lastb);
+                const int in = f < KF ? (f % (2 * NS)) * FH : 32 * HD + ((f - KF) % NT) * FH;
+                __builtin_amdgcn_global_load_lds(kc + (tblk + b) * (64 * HD) + in + lane * 8, l, 16, 0, 0);
+            } else {
+                if (f < KF) {
+                    const int hf = f / (2 * NS), T = (f / NS) & 1, s = f % NS;
+                    const int key = min(kv0 + 32 * hf + 8 * (col >> 2) + 4 * T + (col & 3), ktot - 1);
+                    __builtin_amdgcn_global_load_lds(kc + ((size_t)kh * a.cap + key) * HD + 32 * s + 8 * grp, l, 16,
+                                                     0, 0);
+                } else {
+                    const int fv = f - KF, hf = fv / NT, t = fv % NT;
+                    const int d = 16 * t + col, key0 = kv0 + 32 * hf + 8 * grp;
+                    const uint32_t off = (uint32_t)((((size_t)kh * HD + d) * a.cap + key0) * 2);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, l, 16, off, 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Q as B operands: qb[u][s] holds dims 32s + 8grp + 0..7 of query p0 + 16u + col.
+    const float qsc = a.scale_q ? a.scale : 1.0f;
+    half8 qb[NQT][NS];
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        const int r = min(p0 + 16 * u + col, a.tq - 1);
+        const bool ok = p0 + 16 * u + col < a.tq;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const float4* p = reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 32 * s + 8 * grp);
+            const float4 x0 = p[0], x1 = p[1];
+            const float m = ok ? qsc : 0.0f;
+            half8 x;
+            x[0] = to_h(x0.x * m); x[1] = to_h(x0.y * m); x[2] = to_h(x0.z * m); x[3] = to_h(x0.w * m);
+            x[4] = to_h(x1.x * m); x[5] = to_h(x1.y * m); x[6] = to_h(x1.z * m); x[7] = to_h(x1.w * m);
+            qb[u][s] = x;
+        }
+    }
+
+    floatx4 o[NT][NQT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) o[t][u] = zero_f4();
+    float m[NQT], l[NQT];
+    int ilim[NQT];
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        m[u] = ninf();
+        l[u] = 0.0f;
+        const int r = p0 + 16 * u + col;
+        ilim[u] = a.causal ? min(a.past + r, ktot - 1) : ktot - 1;
+    }
+    const float sl2 = (a.scale_q ? 1.0f : a.scale) * LLMTIE_LOG2E;
+    constexpr float RB = 8.0f;  // log2 headroom before the reference max moves
+
+    // One 64-key tile from LDS buffer `tb`; MASK: some key of it lies past
+    // some row's limit.
+    auto tile = [&](const half_t* tb, int kv0, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const half8* kf = reinterpret_cast<const half8*>(tb);
+        const half8* vf = reinterpret_cast<const half8*>(tb + KF * FH);
+        floatx4 sc[2][2][NQT];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+#pragma unroll
+                for (int u = 0; u < NQT; ++u) sc[hf][T][u] = zero_f4();
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const half8 af = kf[((hf * 2 + T) * NS + s) * 64 + lane];
+#pragma unroll
+                    for (int u = 0; u < NQT; ++u) sc[hf][T][u] = mfma16(af, qb[u][s], sc[hf][T][u]);
+                }
+            }
+        // Software pipeline: PD fragment reads ahead of the MFMAs using them.
+        {
+            constexpr int NR = 4 * NS, PD = 4;
+            __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
+#pragma unroll
+            for (int i2 = 0; i2 < NR - PD; ++i2) {
+                __builtin_amdgcn_sched_group_barrier(0x008, NQT, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NQT * PD, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        half8 pb[2][NQT];
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) {
+            // The reference max m is kept in log2 units and only moves when a
+            // tile's max exceeds it by more than RB (rare after the first
+            // tiles), so O and l are rescaled rarely; in between the
+            // probabilities 2^(score * sl2 - m) are at most 2^RB, well inside
+            // f16, and O / l is unchanged (both carry the same 2^-m).
+            float mx = ninf();
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if constexpr (MASK) {
+                            const int key = kv0 + 32 * hf + 8 * grp + 4 * T + r;
+                            sc[hf][T][u][r] = key <= ilim[u] ? sc[hf][T][u][r] : ninf();
+                        }
+                        mx = fmaxf(mx, sc[hf][T][u][r]);
+                    }
+            mx = max4grp(mx) * sl2;
+            if (__any(mx > m[u] + RB)) {
+                const float mn = fmaxf(m[u], mx);
+                // A row whose every key so far is masked keeps m = -inf.
+                const float fac = mn == ninf() ? 1.0f : ex2(m[u] - mn);
+                m[u] = mn;
+                l[u] *= fac;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) o[t][u] *= fac;
+            }
+            const float msub = m[u] == ninf() ? 0.0f : m[u];
+            float ps = 0.0f;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                half8 p;
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = ex2(__builtin_fmaf(sc[hf][T][u][r], sl2, -msub));
+                        ps += e;
+                        p[4 * T + r] = to_h(e);
+                    }
+                pb[hf][u] = p;
+            }
+            l[u] += ps;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const half8 af = vf[(hf * NT + t) * 64 + lane];
+#pragma unroll
+                for (int u = 0; u < NQT; ++u) o[t][u] = mfma16(af, pb[hf][u], o[t][u]);
+            }
+        {
+            constexpr int NR = 2 * NT, PD = 4;
+            __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
+#pragma unroll
+            for (int i2 = 0; i2 < NR - PD; ++i2) {
+                __builtin_amdgcn_sched_group_barrier(0x008, NQT, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NQT * PD, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Zero the V entries of keys >= ktot in a tile that reaches past ktot.
+    auto zero_tail = [&](half_t* tb, int kv0) {
+        half8* vf = reinterpret_cast<half8*>(tb + KF * FH);
+        for (int c = tid; c < VF * 64; c += PT) {
+            const int hf = c / (NT * 64), ln = c % 64;
+            const int k0 = kv0 + 32 * hf + 8 * (ln >> 4);
+            if (k0 + 8 > ktot) {
+                half8 x = vf[c];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (k0 + j >= ktot) x[j] = (half_t)0.0f;
+                vf[c] = x;
+            }
+        }
+    };
+    auto step = [&](half_t* cur, half_t* nxt, int kv0) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of `cur` have landed
+        __syncthreads();                 // ... and every wave's; `nxt` is free
+        if (kv0 + KT < kend) issue(kv0 + KT, nxt);
+        if (kv0 + KT > ktot) {
+            zero_tail(cur, kv0);
+            __syncthreads();
+        }
+        if (kv0 > wlim) return;
+        if (kv0 + KT - 1 > wall)
+            tile(cur, kv0, std::true_type{});
+        else
+            tile(cur, kv0, std::false_type{});
+    };
+
+    if (kend > 0) issue(0, t0);
+    for (int kv0 = 0; kv0 < kend; kv0 += 2 * KT) {
+        step(t0, t1, kv0);
+        if (kv0 + KT < kend) step(t1, t0, kv0 + KT);
+    }
+
+    // O / l, stored: lane writes dims 16t + 4grp + 0..3 of query p0 + 16u + col.
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        const float lt = sum4grp(l[u]);
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const int r = p0 + 16 * u + col;
+        if (r >= a.tq) continue;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const size_t off = (size_t)r * a.os + (size_t)h * HD + 16 * t + 4 * grp;
+            float4 y = make_float4(o[t][u][0] * inv, o[t][u][1] * inv, o[t][u][2] * inv, o[t][u][3] * inv);
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + off) = y;
+        }
+    }
+}
+
 hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st) {
     const int pb = 16 * nqt * (PW / a.gb);
     dim3 grid((a.tq + pb - 1) / pb, a.heads / a.gb), block(PT);
@@ -380,6 +656,21 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
         return hipGetLastError();                                                            \
     }
 #define LK(HD, KIND) L(HD, KIND, 1) L(HD, KIND, 2) L(HD, KIND, 4)
+    // The f16 caches take the direct-to-LDS kernel when the V cache is
+    // addressable by a 32-bit buffer offset (always, for the tiled cache).
+    // (It keeps the raw-score max, so it needs a positive score scale.)
+    const bool fast = (kind == PF_T16 || (kind == PF_F16 && a.v_bytes <= 0xffffffffull)) &&
+                      (a.scale_q || a.scale > 0.0f) && !getenv("LLMTIE_PREFILL_STAGED");
+    if (fast) {
+#define F(HD, KIND, NQ)                                                                    \
+    if (hd == HD && kind == KIND && nqt == NQ) {                                           \
+        hipLaunchKernelGGL((flash_fwd_kernel<HD, KIND, NQ>), grid, block, 0, st, a);       \
+        return hipGetLastError();                                                          \
+    }
+        F(64, PF_F16, 1) F(64, PF_F16, 2) F(128, PF_F16, 1) F(128, PF_F16, 2)
+        F(64, PF_T16, 1) F(64, PF_T16, 2) F(128, PF_T16, 1) F(128, PF_T16, 2)
+#undef F
+    }
     LK(64, PF_F16) LK(128, PF_F16) LK(64, PF_F32) LK(128, PF_F32) LK(64, PF_ROWS) LK(64, PF_T16) LK(128, PF_T16)
 #undef LK
 #undef L
