@@ -122,6 +122,31 @@ int pick_nqt(size_t tq, size_t heads, int gb) {
     return 1;
 }
 
+// f32 K/V go through the f16 fast kernel via a tiled copy in a stream-ordered
+// workspace (allocated and freed on `st`, so concurrent streams never share
+// it, and capturable in a HIP graph); the staged kernel is the fallback for a
+// non-positive score scale, which the fast kernel does not take.
+int prefill_via_t16(const char* what, hipStream_t st, PrefillArgs a, int hd, int nqt, const float* k, long khs,
+                    long kps, const float* v, long vhs, long vps, long vds, int fallback_kind) {
+    if (!(a.scale_q || a.scale > 0.0f) || getenv("LLMTIE_PREFILL_STAGED"))
+        return launched(what, launch_prefill(hd, fallback_kind, nqt, a, st));
+    const int nkeys = a.past + a.tq;
+    const size_t bytes = (size_t)a.kv_heads * tiled_nblk(nkeys) * 64 * hd * 2;
+    void* ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, bytes, st);
+    if (e != hipSuccess) return driver("hipMallocAsync", e);
+    e = launch_f32_to_t16(k, khs, kps, v, vhs, vps, vds, static_cast<uint16_t*>(ws), a.kv_heads, hd, nkeys, st);
+    if (e == hipSuccess) {
+        a.k = ws;
+        a.v = nullptr;
+        a.cap = nkeys;
+        e = launch_prefill(hd, PF_T16, nqt, a, st);
+    }
+    const hipError_t ef = hipFreeAsync(ws, st);
+    if (e != hipSuccess) return driver(what, e);
+    return launched("hipFreeAsync", ef);
+}
+
 int prefill_common(void* stream, int kind, const float* q, size_t q_len, const void* k, size_t k_len, const void* v,
                    size_t v_len, float* out, size_t out_len, size_t tq, size_t past, size_t heads, size_t kv_heads,
                    size_t hd, size_t cap, float scale, int causal) {
@@ -154,7 +179,14 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
     a.os = (int)(heads * hd);
     a.scale_q = 0;
     a.v_bytes = v_len * (kind == PF_F32 ? 4 : 2);
-    return launched("flash_attn", launch_prefill((int)hd, kind, pick_nqt(tq, heads, gb), a, S(stream)));
+    const int nqt = pick_nqt(tq, heads, gb);
+    if (kind == PF_F32) {
+        const float* kf = static_cast<const float*>(k);
+        const float* vf = static_cast<const float*>(v);
+        return prefill_via_t16("flash_attn", S(stream), a, (int)hd, nqt, kf, (long)(cap * hd), (long)hd, vf,
+                               (long)(hd * cap), 1, (long)cap, PF_F32);
+    }
+    return launched("flash_attn", launch_prefill((int)hd, kind, nqt, a, S(stream)));
 }
 
 // Splits of one head: about `target` workgroups over the whole launch, each
@@ -342,7 +374,9 @@ int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint1
     a.kvs = (int)(3 * d);
     a.os = (int)d;
     a.scale_q = 1;
-    return launched("flash_attn_rows", launch_prefill(64, PF_ROWS, pick_nqt(t, heads, 1), a, S(stream)));
+    a.out_f16 = 1;
+    return prefill_via_t16("flash_attn_rows", S(stream), a, 64, pick_nqt(t, heads, 1), qkv + d, 64, (long)(3 * d),
+                           qkv + 2 * d, 64, (long)(3 * d), 1, PF_ROWS);
 }
 
 int llmtie_attn_decode_f16(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,

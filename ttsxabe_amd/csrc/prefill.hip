@@ -29,6 +29,7 @@
 // LDS rows are XOR-swizzled by 16-byte chunk so that the eight rows one
 // ds_read_b128 phase touches land on distinct banks.
 #include <stdlib.h>
+#include <algorithm>
 #include <type_traits>
 #include "common.h"
 #include "prefill.h"
@@ -641,10 +642,62 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const size_t off = (size_t)r * a.os + (size_t)h * HD + 16 * t + 4 * grp;
-            float4 y = make_float4(o[t][u][0] * inv, o[t][u][1] * inv, o[t][u][2] * inv, o[t][u][3] * inv);
-            *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + off) = y;
+            if (a.out_f16) {
+                half4 y;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[i] = to_h(o[t][u][i] * inv);
+                *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(a.out) + off) = y;
+            } else {
+                float4 y = make_float4(o[t][u][0] * inv, o[t][u][1] * inv, o[t][u][2] * inv, o[t][u][3] * inv);
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + off) = y;
+            }
         }
     }
+}
+
+// One thread per 16-byte chunk of the tiled layout: K chunk (T, s, lane) of
+// a block holds key 8*(col/4) + 4T + col%4, dims 32s + 8grp .. +7; V chunk
+// (t, lane) holds dim 16t + col, keys 8grp .. +7 (kvlayout.h). f32 -> f16 is
+// round to nearest even, as the kernels' own staging does.
+__global__ void f32_to_t16_kernel(const float* __restrict__ k, long khs, long kps, const float* __restrict__ v,
+                                  long vhs, long vps, long vds, half_t* __restrict__ dst, int kv, int hd,
+                                  int nkeys, int nblk) {
+    const int ns = hd / 32, nt = hd / 16;
+    const int bf = 2 * ns + nt;  // chunks-of-64 per block
+    const long total = (long)kv * nblk * bf * 64;
+    for (long c = blockIdx.x * (long)blockDim.x + threadIdx.x; c < total; c += (long)gridDim.x * blockDim.x) {
+        const int lane = c % 64;
+        const long fr = c / 64;
+        const int fi = fr % bf;
+        const long hb = fr / bf;  // (head, block)
+        const int b = hb % nblk, h = hb / nblk;
+        const int col = lane & 15, grp = lane >> 4;
+        half8 x;
+        if (fi < 2 * ns) {
+            const int T = fi / ns, s = fi % ns;
+            const int key = 32 * b + 8 * (col >> 2) + 4 * T + (col & 3);
+            const float* src = k + h * khs + (long)key * kps + 32 * s + 8 * grp;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = key < nkeys ? to_h(src[j]) : (half_t)0.0f;
+        } else {
+            const int t = fi - 2 * ns;
+            const int d = 16 * t + col, k0 = 32 * b + 8 * grp;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                x[j] = k0 + j < nkeys ? to_h(v[h * vhs + (long)(k0 + j) * vps + (long)d * vds]) : (half_t)0.0f;
+        }
+        reinterpret_cast<half8*>(dst)[c] = x;
+    }
+}
+
+hipError_t launch_f32_to_t16(const float* k, long khs, long kps, const float* v, long vhs, long vps, long vds,
+                             uint16_t* dst, int kv, int hd, int nkeys, hipStream_t st) {
+    const int nblk = tiled_nblk(nkeys);
+    const long total = (long)kv * nblk * (2 * (hd / 32) + hd / 16) * 64;
+    const int blocks = (int)std::min<long>((total + 255) / 256, 8192);
+    hipLaunchKernelGGL(f32_to_t16_kernel, dim3(blocks), dim3(256), 0, st, k, khs, kps, v, vhs, vps, vds,
+                       reinterpret_cast<half_t*>(dst), kv, hd, nkeys, nblk);
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st) {
