@@ -342,3 +342,35 @@ def test_decode_q8_batch_is_decode_ref_on_dequantised_cache():
         v = vc[sl].astype(np.float32) * vsc
         want = oracle.decode_ref(q.reshape(nseq, -1)[s], k, v, heads, kv, hd, int(tk[s]), cap, 0.125, False)
         assert np.array_equal(got.reshape(nseq, -1)[s], want)
+
+
+# ------------------------------------------------------------ layer stack
+
+def test_stack_pieces_hand_cases():
+    from oracle.stack import attend, rms_norm, silu_mul
+    y = rms_norm(np.array([[3.0, 4.0]], np.float32), np.array([1.0, 2.0], np.float32), 0.0)
+    assert np.allclose(y, [[3 / np.sqrt(12.5), 8 / np.sqrt(12.5)]], rtol=1e-6)
+    assert np.array_equal(silu_mul(np.zeros(3, np.float32), np.ones(3, np.float32)), np.zeros(3, np.float32))
+    assert np.allclose(silu_mul(np.array([30.0], np.float32), np.array([2.0], np.float32)), [60.0], rtol=1e-6)
+    assert np.allclose(silu_mul(np.array([-1.0], np.float32), np.array([1.0], np.float32)), [-1 / (1 + np.e)])
+    # zero queries: each causal row is the mean of the values it may see
+    kv, hd, past, n = 1, 4, 3, 2
+    k = oracle.seq(kv * 5 * hd, 1).reshape(kv, 5, hd)
+    v = oracle.seq(kv * 5 * hd, 2).reshape(kv, 5, hd)
+    out = attend(np.zeros((n, 2 * hd), np.float32), k, v, past, n, 2, kv, hd, 0.5)
+    assert np.allclose(out[0, :hd], v[0, :4].mean(0), atol=1e-6)
+    assert np.allclose(out[1, hd:], v[0, :5].mean(0), atol=1e-6)
+
+
+def test_stack_with_silent_blocks_is_norm_then_head():
+    from oracle.stack import CpuStack, StackConfig, random_weights
+    cfg = StackConfig(vocab=64, hidden=128, heads=2, kv_heads=1, head_dim=64, ffn=64, layers=1)
+    w = random_weights(cfg, 3)
+    w["0.wo"][:] = 0.0   # attention contributes nothing
+    w["0.wd"][:] = 0.0   # nor does the feed-forward
+    s = CpuStack(cfg, w)
+    got = s.forward([5, 9, 17])
+    x = w["embed"][17].astype(np.float64)
+    want = (x / np.sqrt((x * x).mean() + cfg.eps) * w["norm"]) @ w["lm_head"].T.astype(np.float64)
+    assert np.abs(got - want).max() < 1e-4 * np.abs(want).max()
+    assert s.past == 3 and s.k[0].shape == (1, 3, 64)

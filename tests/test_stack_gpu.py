@@ -1,0 +1,47 @@
+"""The attention path inside a random-init Llama stack: greedy decode on the
+GPU (ttsxabe_amd.stack: torch projections, this library's RoPE, cache writes,
+growth and attention) against the CPU restatement of the same stack
+(oracle/stack.py), token by token.
+
+The reference's own end-to-end check is the chat model's argmax against a
+captured run of the original (crates/llmtie-chat/tests/stepwise.rs); with no
+checkpoint here, the same check runs on random weights. The prompt is 250
+tokens so decoding crosses the 256-position cache capacity and exercises the
+growth path. Tolerances: the GPU rounds q and the probabilities to f16 in the
+prefill (the reference's flash arithmetic), so logits agree to ~1e-3 of their
+scale, not bit for bit; the GPU's argmax must be one of the CPU's near-ties
+within twice the measured logit error, and both sides continue from the CPU's
+token so one near-tie cannot cascade.
+"""
+import numpy as np
+import pytest
+
+from oracle.stack import CpuStack, StackConfig, random_weights
+
+from tests.configs import SEED
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("layout", ["reference", "tiled"])
+def test_random_llama_stack_decodes_like_the_cpu(gpu, layout):
+    from ttsxabe_amd.stack import LlamaStack
+    cfg = StackConfig()
+    w = random_weights(cfg, SEED)
+    cpu = CpuStack(cfg, w)
+    dev = LlamaStack(gpu, cfg, w, layout)
+    rng = np.random.default_rng(SEED + 1)
+    ids = [int(t) for t in rng.integers(0, cfg.vocab, 250)]
+    exact = 0
+    for step in range(12):
+        lc = cpu.forward(ids)
+        lg = dev.forward(ids).float().cpu().numpy()
+        scale = float(np.abs(lc).max())
+        err = float(np.abs(lc - lg).max())
+        assert err < 5e-3 * scale, f"{layout} step {step}: logit error {err:.3g} of scale {scale:.3g}"
+        top_c, top_g = int(lc.argmax()), int(lg.argmax())
+        assert lc[top_g] >= lc[top_c] - 2 * err - 1e-6, f"{layout} step {step}: GPU argmax {top_g} is no CPU near-tie"
+        exact += top_c == top_g
+        ids = [top_c]
+    assert dev.past == cpu.past == 261 and dev.cap == 512
+    assert exact >= 10, f"{layout}: only {exact} of 12 argmaxes equal"
