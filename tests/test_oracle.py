@@ -374,3 +374,23 @@ def test_stack_with_silent_blocks_is_norm_then_head():
     want = (x / np.sqrt((x * x).mean() + cfg.eps) * w["norm"]) @ w["lm_head"].T.astype(np.float64)
     assert np.abs(got - want).max() < 1e-4 * np.abs(want).max()
     assert s.past == 3 and s.k[0].shape == (1, 3, 64)
+
+
+def test_cross_cache_ref_brute_force():
+    from oracle.whisper import cross_cache_ref
+    t, d, heads, layers = 3, 4, 2, 2
+    rng = np.random.default_rng(5)
+    enc = rng.standard_normal((t, d)).astype(np.float32)
+    wk = rng.standard_normal((layers, d, d)).astype(np.float32)
+    wv = rng.standard_normal((layers, d, d)).astype(np.float32)
+    bv = rng.standard_normal((layers, d)).astype(np.float32)
+    got = cross_cache_ref(enc, wk, wv, bv, heads)
+    h16 = lambda a: np.float64(np.float16(a))
+    for l in range(layers):
+        for p in range(t):
+            for o in range(d):
+                ks = sum(h16(enc[p, i]) * h16(wk[l, o, i]) for i in range(d))
+                vs = np.float32(sum(h16(enc[p, i]) * h16(wv[l, o, i]) for i in range(d))) + bv[l, o]
+                h, j = divmod(o, d // heads)
+                assert got[l][0][h, p, j] == np.float16(np.float32(ks)).view(np.uint16)
+                assert got[l][1][h, j, p] == np.float16(np.float32(vs)).view(np.uint16)

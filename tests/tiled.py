@@ -54,6 +54,19 @@ def pack_t16(k, v, kv: int, hd: int, cap: int, live: int | None = None) -> np.nd
     return out.ravel()
 
 
+def unpack_t16(data, kv: int, hd: int, cap: int):
+    """Inverse of pack_t16: tiled uint16 -> (K [kv][cap][hd], V [kv][hd][cap])."""
+    nblk = (cap + 31) // 32
+    d = np.asarray(data, np.uint16).reshape(kv, nblk, 2, 32 * hd)
+    key_k, dim_k, key_v, dim_v = t16_index(hd)
+    kk = np.zeros((kv, nblk * 32, hd), np.uint16)
+    vv = np.zeros((kv, hd, nblk * 32), np.uint16)
+    for b in range(nblk):
+        kk[:, 32 * b + key_k, dim_k] = d[:, b, 0]
+        vv[:, dim_v, 32 * b + key_v] = d[:, b, 1]
+    return np.ascontiguousarray(kk[:, :cap]), np.ascontiguousarray(vv[:, :, :cap])
+
+
 def q8_block_bytes(hd: int) -> int:
     return 2 * 32 * hd + 2 * 32 * (hd // 32) * 2
 
