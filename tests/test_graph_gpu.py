@@ -1,0 +1,71 @@
+"""HIP-graph capture of the path, as bench.py times it: every replay, with
+the program's own eager work and synchronisations between replays, must give
+the eager result bit for bit. Covers the decode's split hand-off (arrival
+counters left at zero by every call, so a replay starts clean), the two-phase
+merge, the prefill, and the f32 prefill's stream-ordered workspace
+(allocated and freed inside the graph)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.util import up, up_f16
+
+pytestmark = pytest.mark.gpu
+
+
+def _replays_match(fn, n=4):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        eager = [t.clone() for t in fn()]
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            outs = fn()
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(n):
+        # unrelated eager work and a sync between replays
+        junk = torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(eager, outs):
+            assert torch.equal(a, b), f"replay {i} differs from the eager result"
+        del junk
+
+
+@pytest.mark.parametrize("two_phase", ["0", "1"])
+def test_decode_graph_replays(gpu, two_phase, monkeypatch):
+    from ttsxabe_amd.gpu import DecodeScratch, TiledCache16
+    monkeypatch.setenv("LLMTIE_DECODE_TWO_PHASE", two_phase)
+    heads, kv, hd, tk, cap = 32, 8, 128, 4000, 4096
+    q = up(oracle.seq(heads * hd, 1))
+    k = up_f16(oracle.seq(kv * cap * hd, 2))
+    v = up_f16(oracle.seq(kv * cap * hd, 3))
+    t = TiledCache16(kv, hd, cap)
+    gpu.t16_from_ref(k, v, t, tk)
+    s1, s2 = DecodeScratch(), DecodeScratch()
+    _replays_match(lambda: [gpu.attn_decode_f16(q, k, v, heads, kv, hd, tk, cap, 0.088, False, s1),
+                            gpu.attn_decode_t16(q, t, heads, tk, 0.088, False, s2)])
+
+
+def test_prefill_graph_replays(gpu):
+    heads, kv, hd, tq, cap = 32, 8, 128, 300, 512
+    q = up(oracle.seq(tq * heads * hd, 4))
+    k16 = up_f16(oracle.seq(kv * cap * hd, 5))
+    v16 = up_f16(oracle.seq(kv * cap * hd, 6))
+    k32 = up(oracle.seq(kv * cap * hd, 5))
+    v32 = up(oracle.seq(kv * cap * hd, 6))
+    _replays_match(lambda: [gpu.flash_attn_f16(q, k16, v16, tq, 0, heads, kv, hd, cap, 0.088, True),
+                            gpu.flash_attn(q, k32, v32, tq, 0, heads, kv, hd, cap, 0.088, True)])
+
+
+def test_encoder_rows_graph_replays(gpu):
+    t, heads, hd = 1500, 20, 64
+    qkv = up(oracle.seq(t * 3 * heads * hd, 7))
+    _replays_match(lambda: [gpu.flash_attn_rows(qkv, t, heads, hd, 0.125)])
