@@ -534,9 +534,9 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     constexpr int NS = HD / 32;
     constexpr int NT = HD / 16;
     constexpr bool TILED = KIND == KV_T16 || KIND == KV_TQ8;
-    constexpr int OBS = HD * 17;  // one wave's O^T in LDS, padded
-    __shared__ float lds[DW * OBS];
-    __shared__ float wm[DW][16], wl[DW][16], gm[16], gl[16];
+    constexpr int OBW = 16 * (HD + 4);  // one wave's O^T in LDS, [column][dim], padded
+    __shared__ float lds[DW * OBW];
+    __shared__ float wm[DW][16], wl[DW][16], gl[16];
     __shared__ int last;
 
     const int tid = threadIdx.x;
@@ -655,32 +655,27 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     }
     l_run = sum4grp(l_run);
 
-    // Combine the four waves: M = max m_w, each wave's O scaled by 2^(m_w - M).
+    // Combine the four waves: each wave leaves its (m, l) and its unscaled
+    // O^T in LDS ([query column][dim], 16-byte writes), one barrier, and the
+    // combining reads weight wave w by 2^(m_w - M), M = max_w m_w.
     if (grp == 0) {
         wm[wave][col] = m_run;
         wl[wave][col] = l_run;
     }
-    __syncthreads();
-    float M = ninf();
-#pragma unroll
-    for (int w = 0; w < DW; ++w) M = fmaxf(M, wm[w][col]);
-    const float myf = (m_run == ninf()) ? 0.0f : ex2(m_run - M);
-    float* ob = lds + wave * OBS;
+    float* ob = lds + wave * OBW;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ob[(16 * t + 4 * grp + r) * 17 + col] = o[t][r] * myf;
-    if (tid < 16) {
-        float L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < DW; ++w) {
-            const float mw = wm[w][tid];
-            L += (mw == ninf()) ? 0.0f : wl[w][tid] * ex2(mw - M);
-        }
-        gm[tid] = M;
-        gl[tid] = L;
-    }
+        *reinterpret_cast<floatx4*>(&ob[col * (HD + 4) + 16 * t + 4 * grp]) = o[t];
     __syncthreads();
+    // Wave weights of query column g, and its combined normaliser.
+    auto weights = [&](int g, float (&f)[DW]) {
+        float M = ninf();
+#pragma unroll
+        for (int w = 0; w < DW; ++w) M = fmaxf(M, wm[w][g]);
+#pragma unroll
+        for (int w = 0; w < DW; ++w) f[w] = wm[w][g] == ninf() ? 0.0f : ex2(wm[w][g] - M);
+        return M;
+    };
 
     float* out = a.out + a.out_off + (size_t)seq * a.out_stride;
     int8_t* tc = nullptr;
@@ -694,31 +689,49 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     if (nsplit == 1) {
         for (int e = tid; e < n; e += DT) {
             const int g = e / HD, d = e % HD;
-            float acc = 0.0f;
+            float f[DW];
+            weights(g, f);
+            float acc = 0.0f, L = 0.0f;
 #pragma unroll
-            for (int w = 0; w < DW; ++w) acc += lds[w * OBS + d * 17 + g];
-            emit(out, tc, ts, (size_t)h * group * HD + e, acc / gl[g]);
+            for (int w = 0; w < DW; ++w) {
+                acc += lds[w * OBW + g * (HD + 4) + d] * f[w];
+                L += wl[w][g] * f[w];
+            }
+            emit(out, tc, ts, (size_t)h * group * HD + e, acc / L);
         }
         return;
     }
 
     // Publish this split's partial: O [g][HD] (relative to its own max) in
-    // the O area, (m, l) per g in the ML area.
+    // the O area, (m, l) per g in the ML area, 16 bytes a store.
     const size_t head = (size_t)seq * gridDim.y + h;
     float* po = a.part + (head * a.splits) * n;
     float* pml = a.part + a.ml_off + (head * a.splits) * group * 2;
+    auto partial4 = [&](int e4) {
+        const int g = (4 * e4) / HD, d = (4 * e4) % HD;
+        float f[DW];
+        weights(g, f);
+        floatx4 acc = zero_f4();
+#pragma unroll
+        for (int w = 0; w < DW; ++w) acc += *reinterpret_cast<const floatx4*>(&lds[w * OBW + g * (HD + 4) + d]) * f[w];
+        return acc;
+    };
+    auto ml = [&](int g) {
+        float f[DW];
+        const float M = weights(g, f);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < DW; ++w) L += wl[w][g] * f[w];
+        return floatx4{M, L, 0.0f, 0.0f};
+    };
     if (a.two_phase) {
         // A separate merge launch follows: plain stores, and done.
-        for (int e = tid; e < n; e += DT) {
-            const int g = e / HD, d = e % HD;
-            float acc = 0.0f;
-#pragma unroll
-            for (int w = 0; w < DW; ++w) acc += lds[w * OBS + d * 17 + g];
-            po[(size_t)split * n + e] = acc;
-        }
+        for (int e4 = tid; e4 < n / 4; e4 += DT)
+            *reinterpret_cast<floatx4*>(po + (size_t)split * n + 4 * e4) = partial4(e4);
         if (tid < group) {
-            pml[((size_t)split * group + tid) * 2] = gm[tid];
-            pml[((size_t)split * group + tid) * 2 + 1] = gl[tid];
+            const floatx4 x = ml(tid);
+            pml[((size_t)split * group + tid) * 2] = x[0];
+            pml[((size_t)split * group + tid) * 2 + 1] = x[1];
         }
         return;
     }
@@ -728,16 +741,20 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     // partials with agent-scope loads. A release/acquire fence pair would
     // write back and invalidate the whole L2 of the XCD on every workgroup,
     // which measured several times the cost of the attention itself.
-    for (int e = tid; e < n; e += DT) {
-        const int g = e / HD, d = e % HD;
-        float acc = 0.0f;
-#pragma unroll
-        for (int w = 0; w < DW; ++w) acc += lds[w * OBS + d * 17 + g];
-        st_coherent(po + (size_t)split * n + e, acc);
+    {
+        const __amdgpu_buffer_rsrc_t rp =
+            __builtin_amdgcn_make_buffer_rsrc(po + (size_t)split * n, 0, n * 4, 0x00020000);
+        typedef float v4 __attribute__((ext_vector_type(4)));
+        for (int e4 = tid; e4 < n / 4; e4 += DT) {
+            const floatx4 x = partial4(e4);
+            const v4 y = {x[0], x[1], x[2], x[3]};
+            __builtin_amdgcn_raw_buffer_store_b128(y, rp, e4 * 16, 0, 16);  // sc1: agent scope
+        }
     }
     if (tid < group) {
-        st_coherent(pml + ((size_t)split * group + tid) * 2, gm[tid]);
-        st_coherent(pml + ((size_t)split * group + tid) * 2 + 1, gl[tid]);
+        const floatx4 x = ml(tid);
+        st_coherent(pml + ((size_t)split * group + tid) * 2, x[0]);
+        st_coherent(pml + ((size_t)split * group + tid) * 2 + 1, x[1]);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
