@@ -83,7 +83,12 @@ int llmtie_supports_flash(size_t head_dim, size_t heads, size_t kv_heads);
 
 /* Gpu::flash_attn (device.rs:5702): causal or full attention of tq query rows
  * (positions past .. past+tq-1) against an f32 cache holding past+tq keys.
- * out = [tq, heads*head_dim] f32. */
+ * out = [tq, heads*head_dim] f32.
+ * This and llmtie_flash_attn_rows stage the f32 keys and values as a tiled f16
+ * copy in a library-owned workspace, one per (device, stream), grown on demand
+ * and never freed before the process ends. Calls ordered on one stream share
+ * it; a HIP graph captured from a stream uses that stream's workspace, so its
+ * replays must not overlap other calls made on the capturing stream. */
 int llmtie_flash_attn(void* stream, const float* q, size_t q_len, const float* k, size_t k_len,
                       const float* v, size_t v_len, float* out, size_t out_len, size_t tq, size_t past,
                       size_t heads, size_t kv_heads, size_t head_dim, size_t cap, float scale, int causal);

@@ -9,6 +9,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "../../include/llmtie_hip.h"
 #include "decode.h"
@@ -122,27 +124,67 @@ int pick_nqt(size_t tq, size_t heads, int gb) {
     return 1;
 }
 
-// f32 K/V go through the f16 fast kernel via a tiled copy in a stream-ordered
-// workspace (allocated and freed on `st`, so concurrent streams never share
-// it, and capturable in a HIP graph); the staged kernel is the fallback for a
-// non-positive score scale, which the fast kernel does not take.
+// Workspace for the tiled f16 copy of f32 K/V: one grow-only buffer per
+// (device, stream), so calls ordered on a stream share it and concurrent
+// streams never do. A buffer is never freed or reallocated in place (a
+// captured HIP graph may hold its address): growth allocates a larger one
+// and keeps the old alive until the process ends. Growth is not possible
+// while the stream is capturing; the caller then falls back to a
+// stream-ordered allocation inside the graph.
+struct Workspace {
+    int device;
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
+};
+std::mutex ws_mutex;
+std::vector<Workspace> ws_list;
+
+void* cached_workspace(hipStream_t st, size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(ws_mutex);
+    for (Workspace& w : ws_list)
+        if (w.device == dev && w.stream == st && w.bytes >= bytes) return w.ptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    void* p = nullptr;
+    const size_t want = std::max<size_t>(bytes, (size_t)1 << 20);
+    if (hipMalloc(&p, want) != hipSuccess) return nullptr;
+    for (Workspace& w : ws_list)
+        if (w.device == dev && w.stream == st) {
+            w.ptr = p;  // the old buffer stays allocated (see above)
+            w.bytes = want;
+            return p;
+        }
+    ws_list.push_back(Workspace{dev, st, p, want});
+    return p;
+}
+
+// f32 K/V go through the f16 fast kernel via a tiled f16 copy in a
+// workspace; the staged kernel is the fallback for a non-positive score
+// scale, which the fast kernel does not take.
 int prefill_via_t16(const char* what, hipStream_t st, PrefillArgs a, int hd, int nqt, const float* k, long khs,
                     long kps, const float* v, long vhs, long vps, long vds, int fallback_kind) {
     if (!(a.scale_q || a.scale > 0.0f) || getenv("LLMTIE_PREFILL_STAGED"))
         return launched(what, launch_prefill(hd, fallback_kind, nqt, a, st));
     const int nkeys = a.past + a.tq;
     const size_t bytes = (size_t)a.kv_heads * tiled_nblk(nkeys) * 64 * hd * 2;
-    void* ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, bytes, st);
-    if (e != hipSuccess) return driver("hipMallocAsync", e);
-    e = launch_f32_to_t16(k, khs, kps, v, vhs, vps, vds, static_cast<uint16_t*>(ws), a.kv_heads, hd, nkeys, st);
+    void* ws = cached_workspace(st, bytes);
+    const bool ordered = ws == nullptr;
+    if (ordered) {
+        hipError_t e = hipMallocAsync(&ws, bytes, st);
+        if (e != hipSuccess) return driver("hipMallocAsync", e);
+    }
+    hipError_t e = launch_f32_to_t16(k, khs, kps, v, vhs, vps, vds, static_cast<uint16_t*>(ws), a.kv_heads, hd,
+                                     nkeys, st);
     if (e == hipSuccess) {
         a.k = ws;
         a.v = nullptr;
         a.cap = nkeys;
         e = launch_prefill(hd, PF_T16, nqt, a, st);
     }
-    const hipError_t ef = hipFreeAsync(ws, st);
+    const hipError_t ef = ordered ? hipFreeAsync(ws, st) : hipSuccess;
     if (e != hipSuccess) return driver(what, e);
     return launched("hipFreeAsync", ef);
 }

@@ -655,49 +655,83 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     }
 }
 
-// One thread per 16-byte chunk of the tiled layout: K chunk (T, s, lane) of
-// a block holds key 8*(col/4) + 4T + col%4, dims 32s + 8grp .. +7; V chunk
-// (t, lane) holds dim 16t + col, keys 8grp .. +7 (kvlayout.h). f32 -> f16 is
-// round to nearest even, as the kernels' own staging does.
-__global__ void f32_to_t16_kernel(const float* __restrict__ k, long khs, long kps, const float* __restrict__ v,
-                                  long vhs, long vps, long vds, half_t* __restrict__ dst, int kv, int hd,
-                                  int nkeys, int nblk) {
-    const int ns = hd / 32, nt = hd / 16;
-    const int bf = 2 * ns + nt;  // chunks-of-64 per block
-    const long total = (long)kv * nblk * bf * 64;
-    for (long c = blockIdx.x * (long)blockDim.x + threadIdx.x; c < total; c += (long)gridDim.x * blockDim.x) {
-        const int lane = c % 64;
-        const long fr = c / 64;
-        const int fi = fr % bf;
-        const long hb = fr / bf;  // (head, block)
-        const int b = hb % nblk, h = hb / nblk;
-        const int col = lane & 15, grp = lane >> 4;
-        half8 x;
-        if (fi < 2 * ns) {
-            const int T = fi / ns, s = fi % ns;
-            const int key = 32 * b + 8 * (col >> 2) + 4 * T + (col & 3);
-            const float* src = k + h * khs + (long)key * kps + 32 * s + 8 * grp;
+// One workgroup per (head, 32-key block): the block's K rows and V rows (or
+// V^T rows) are read with coalesced 16-byte loads into LDS, then written out
+// as the tiled layout's 16-byte chunks -- K chunk (T, s, lane) holds key
+// 8*(col/4) + 4T + col%4, dims 32s + 8grp .. +7; V chunk (t, lane) holds dim
+// 16t + col, keys 8grp .. +7 (kvlayout.h). f32 -> f16 rounds to nearest
+// even, as the kernels' own staging does. VKEY: V is stored keys-contiguous
+// (V^T rows, the f32 cache); otherwise dims-contiguous (stacked rows).
+template <int HD, bool VKEY>
+__global__ __launch_bounds__(256) void f32_to_t16_kernel(const float* __restrict__ k, long khs, long kps,
+                                                         const float* __restrict__ v, long vhs, long vps, long vds,
+                                                         half_t* __restrict__ dst, int nkeys, int nblk) {
+    constexpr int NS = HD / 32, NT = HD / 16;
+    __shared__ float ks[32][HD + 1];
+    __shared__ float vs[VKEY ? HD : 32][VKEY ? 33 : HD + 1];
+    const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int live = min(32, nkeys - 32 * b);  // keys of this block that exist
+    // K rows: 32 x HD floats, float4 per thread-step.
+    for (int i = tid; i < 32 * HD / 4; i += 256) {
+        const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < live) x = *reinterpret_cast<const float4*>(k + h * khs + (long)(32 * b + r) * kps + c);
+        ks[r][c] = x.x; ks[r][c + 1] = x.y; ks[r][c + 2] = x.z; ks[r][c + 3] = x.w;
+    }
+    if constexpr (VKEY) {
+        // V^T rows: HD x 32 keys, keys contiguous.
+        for (int i = tid; i < HD * 8; i += 256) {
+            const int d = i / 8, c = 4 * (i % 8);
+            const float* src = v + h * vhs + (long)d * vds + 32 * b + c;
+            float x[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = key < nkeys ? to_h(src[j]) : (half_t)0.0f;
-        } else {
-            const int t = fi - 2 * ns;
-            const int d = 16 * t + col, k0 = 32 * b + 8 * grp;
+            for (int j = 0; j < 4; ++j) x[j] = c + j < live ? src[j] : 0.0f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                x[j] = k0 + j < nkeys ? to_h(v[h * vhs + (long)(k0 + j) * vps + (long)d * vds]) : (half_t)0.0f;
+            for (int j = 0; j < 4; ++j) vs[d][c + j] = x[j];
         }
-        reinterpret_cast<half8*>(dst)[c] = x;
+    } else {
+        for (int i = tid; i < 32 * HD / 4; i += 256) {
+            const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
+            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < live) x = *reinterpret_cast<const float4*>(v + h * vhs + (long)(32 * b + r) * vps + c);
+            vs[r][c] = x.x; vs[r][c + 1] = x.y; vs[r][c + 2] = x.z; vs[r][c + 3] = x.w;
+        }
+    }
+    __syncthreads();
+    half8* out = reinterpret_cast<half8*>(dst) + ((size_t)h * nblk + b) * (2 * NS + NT) * 64;
+    for (int c = tid; c < 2 * NS * 64; c += 256) {
+        const int ln = c % 64, col = ln & 15, grp = ln >> 4, f = c / 64, T = f / NS, s = f % NS;
+        const int key = 8 * (col >> 2) + 4 * T + (col & 3);
+        half8 x;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = to_h(ks[key][32 * s + 8 * grp + j]);
+        out[c] = x;
+    }
+    for (int c = tid; c < NT * 64; c += 256) {
+        const int ln = c % 64, col = ln & 15, grp = ln >> 4, t = c / 64;
+        const int d = 16 * t + col;
+        half8 x;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = to_h(VKEY ? vs[d][8 * grp + j] : vs[8 * grp + j][d]);
+        out[2 * NS * 64 + c] = x;
     }
 }
 
 hipError_t launch_f32_to_t16(const float* k, long khs, long kps, const float* v, long vhs, long vps, long vds,
                              uint16_t* dst, int kv, int hd, int nkeys, hipStream_t st) {
     const int nblk = tiled_nblk(nkeys);
-    const long total = (long)kv * nblk * (2 * (hd / 32) + hd / 16) * 64;
-    const int blocks = (int)std::min<long>((total + 255) / 256, 8192);
-    hipLaunchKernelGGL(f32_to_t16_kernel, dim3(blocks), dim3(256), 0, st, k, khs, kps, v, vhs, vps, vds,
-                       reinterpret_cast<half_t*>(dst), kv, hd, nkeys, nblk);
-    return hipGetLastError();
+    const dim3 grid(nblk, kv);
+    half_t* d = reinterpret_cast<half_t*>(dst);
+    const bool vkey = vps == 1;
+#define CV(HD, VK)                                                                                      \
+    if (hd == HD && vkey == VK) {                                                                       \
+        hipLaunchKernelGGL((f32_to_t16_kernel<HD, VK>), grid, dim3(256), 0, st, k, khs, kps, v, vhs, vps, vds, d, \
+                           nkeys, nblk);                                                                \
+        return hipGetLastError();                                                                       \
+    }
+    CV(64, false) CV(64, true) CV(128, false) CV(128, true)
+#undef CV
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st) {
