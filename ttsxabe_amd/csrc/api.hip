@@ -231,6 +231,19 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
     return launched("flash_attn", launch_prefill((int)hd, kind, nqt, a, S(stream)));
 }
 
+// Compute units of the current device (cached per device).
+int compute_units() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 // Splits of one head: about `target` workgroups over the whole launch, each
 // wave taking whole 32-key blocks, and never more than the merge can hold.
 void plan_decode(size_t tk_max, size_t units, size_t group, int& nit, int& splits) {
@@ -477,6 +490,22 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     const size_t group = heads / kv_heads;
     int nit, splits;
     plan_decode(max_tk, kv_heads * nseq, group, nit, splits);
+    // Up to 64 sequences are planned on the device from their real lengths
+    // (the host knows only max_tk): a 1-D grid of two workgroups per compute
+    // unit, every one resident at once, each running one equal-sized item.
+    const bool dyn = nseq <= 64 && !getenv("LLMTIE_DECODE_STATIC");
+    int nit_max = 0, items = 0;
+    if (dyn) {
+        const size_t max_splits =
+            std::min<size_t>(DECODE_MAX_SPLITS, DECODE_MAX_SPLIT_ROWS / std::max<size_t>(1, group));
+        nit = 1;  // smallest blocks-per-wave whose splits the merge can hold
+        while ((max_tk + 128 * (size_t)nit - 1) / (128 * (size_t)nit) > max_splits) ++nit;
+        nit_max = (int)std::max<size_t>((size_t)nit, (max_tk + 127) / 128);
+        splits = (int)((max_tk + 128 * (size_t)nit - 1) / (128 * (size_t)nit));
+        int per_cu = 2;
+        if (const char* e = getenv("LLMTIE_DECODE_ITEMS_PER_CU")) per_cu = std::max(1, atoi(e));
+        items = std::max(per_cu * compute_units(), (int)(kv_heads * nseq));
+    }
     const size_t part = nseq * kv_heads * (size_t)splits * group * (head_dim + 2);
     const long ml_off = (long)(nseq * kv_heads * (size_t)splits * group * head_dim);
     int r = ensure_scratch(scratch, part, nseq * kv_heads, S(stream));
@@ -502,7 +531,15 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     a.qscale = scale_q ? scale : 1.0f;
     a.nit = nit;
     a.splits = splits;
-    a.two_phase = two_phase_merge(splits, kv_heads * nseq);
+    // A device-planned batch merges in-launch (measured faster at C5 than a
+    // second launch: each head has few splits, and its last arriver merges
+    // while the rest of the batch still streams).
+    a.two_phase = dyn ? (getenv("LLMTIE_DECODE_TWO_PHASE") ? two_phase_merge(items, 1) : 0)
+                      : two_phase_merge(splits, kv_heads * nseq);
+    a.dyn = dyn ? 1 : 0;
+    a.nseq = (int)nseq;
+    a.items = items;
+    a.nit_max = nit_max;
     return launched("attn_decode_q8_batch", launch_decode((int)head_dim, KV_TQ8, a, (int)kv_heads, (int)nseq, S(stream)));
 }
 

@@ -36,6 +36,13 @@ struct DecodeArgs {
     int nit;                 // 32-key blocks per wave per split
     int splits;              // grid.x: splits of the longest sequence
     int two_phase;           // merge in a second launch (else the last split's workgroup merges)
+    // Batched sequences planned on the device (dyn != 0): the launch is a 1-D
+    // grid of `items` workgroups; every workgroup reads the batch's lengths,
+    // takes the smallest blocks-per-wave in [nit, nit_max] whose work items
+    // (kv heads x splits of every sequence) fit in `items`, and runs the item
+    // its index names (sequence-major, then split, then kv head). `splits`
+    // is then the largest split count any plan can give (the scratch stride).
+    int dyn, nseq, items, nit_max;
 };
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);

@@ -529,6 +529,36 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
     }
 }
 
+
+// Device-side plan of a batched launch (DecodeArgs::dyn). Lane l of the wave
+// holds sequence l's effective length (nseq <= 64): its live length, clamped
+// to the launch bound, or 1 for a sequence the batch describes wrongly (it
+// still gets one item, to write its NaN row).
+__device__ __forceinline__ int dyn_len(const DecodeArgs& a, int lane) {
+    if (lane >= a.nseq) return 0;
+    const int tk = min(a.tk_arr[lane], a.tk);
+    const int slot = a.slot_arr[lane];
+    return (slot < 0 || slot >= a.slots || tk <= 0) ? 1 : tk;
+}
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+// Smallest blocks-per-wave n in [a.nit, a.nit_max] with kv x sum of
+// ceil(len / span(n)) <= a.items (the host guarantees it holds at nit_max).
+__device__ __forceinline__ int dyn_nit(const DecodeArgs& a, int len, int nw) {
+    int lo = a.nit, hi = a.nit_max;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        const int span = nw * mid * 32;
+        const int items = a.kv_heads * wave_sum(len > 0 ? (len + span - 1) / span : 0);
+        if (items <= a.items) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
 template <int HD, int KIND, int VA>
 __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel(DecodeArgs a) {
     constexpr int NS = HD / 32;
@@ -542,7 +572,28 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
-    const int split = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
+    int split = blockIdx.x, h = blockIdx.y, seq = blockIdx.z, nit = a.nit;
+    if (a.dyn) {
+        const int len = dyn_len(a, lane);
+        nit = dyn_nit(a, len, DW);
+        const int span = DW * nit * 32;
+        // This workgroup's item: sequence-major prefix sums of kv x splits.
+        const int cnt = len > 0 ? a.kv_heads * ((len + span - 1) / span) : 0;
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        const int item = blockIdx.x;
+        const unsigned long long past = __ballot(incl <= item);  // sequences wholly before the item
+        seq = __popcll(past);
+        if (seq >= a.nseq) return;  // a spare workgroup: the plan needs fewer items
+        const int before = __shfl(incl - cnt, seq, 64);
+        const int r = item - before;
+        split = r / a.kv_heads;
+        h = r % a.kv_heads;
+    }
     const int group = a.group;
     const int tk = a.tk_arr ? min(a.tk_arr[seq], a.tk) : a.tk;
     const int slot = a.slot_arr ? a.slot_arr[seq] : 0;
@@ -554,7 +605,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
                 a.out[a.out_off + (size_t)seq * a.out_stride + (size_t)h * group * HD + e] = __builtin_nanf("");
         return;
     }
-    const int span = DW * a.nit * 32;
+    const int span = DW * nit * 32;
     const int nsplit = (tk + span - 1) / span;
     if (split >= nsplit) return;  // whole workgroup: a shorter sequence of the batch
 
@@ -577,10 +628,10 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     // through a two-deep pipeline (block i+1's loads in flight while block i
     // is folded), then the context's one partial block if it is this wave's.
     // The first block's loads go out before the queries are read.
-    const int first = split * DW * a.nit + wave;
+    const int first = split * DW * nit + wave;
     const int nfull = tk >> 5;
-    const int nf = nfull > first ? min(a.nit, (nfull - first + DW - 1) / DW) : 0;
-    const bool tail = (tk & 31) && nfull >= first && (nfull - first) % DW == 0 && (nfull - first) / DW < a.nit;
+    const int nf = nfull > first ? min(nit, (nfull - first + DW - 1) / DW) : 0;
+    const bool tail = (tk & 31) && nfull >= first && (nfull - first) % DW == 0 && (nfull - first) / DW < nit;
     Frag<HD, KIND> f0, f1;
     if (nf > 0) load_block<HD, KIND, VA, true>(c, first * 32, lane, f0);
 
@@ -704,7 +755,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
 
     // Publish this split's partial: O [g][HD] (relative to its own max) in
     // the O area, (m, l) per g in the ML area, 16 bytes a store.
-    const size_t head = (size_t)seq * gridDim.y + h;
+    const size_t head = (size_t)seq * a.kv_heads + h;
     float* po = a.part + (head * a.splits) * n;
     float* pml = a.part + a.ml_off + (head * a.splits) * group * 2;
     auto partial4 = [&](int e4) {
@@ -781,11 +832,12 @@ __global__ __launch_bounds__(DT) void attn_merge_kernel(DecodeArgs a) {
     const int tk = a.tk_arr ? min(a.tk_arr[seq], a.tk) : a.tk;
     const int slot = a.slot_arr ? a.slot_arr[seq] : 0;
     if (a.slot_arr && (slot < 0 || slot >= a.slots || tk <= 0)) return;
-    const int span = DW * a.nit * 32;
+    const int nit = a.dyn ? dyn_nit(a, dyn_len(a, threadIdx.x & 63), DW) : a.nit;
+    const int span = DW * nit * 32;
     const int nsplit = (tk + span - 1) / span;
     if (nsplit <= 1) return;  // the attention launch wrote this head itself
     const int n = group * HD;
-    const size_t head = (size_t)seq * gridDim.x + h;
+    const size_t head = (size_t)seq * a.kv_heads + h;
     const float* po = a.part + (head * a.splits) * n;
     const float* pml = a.part + a.ml_off + (head * a.splits) * group * 2;
     float* out = a.out + a.out_off + (size_t)seq * a.out_stride;
@@ -815,7 +867,8 @@ static hipError_t launch_merge(int hd, const DecodeArgs& a, int kv_heads, int ns
 }
 
 static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
-    dim3 grid(a.splits, kv_heads, nseq), block(DT);
+    dim3 grid = a.dyn ? dim3(a.items) : dim3(a.splits, kv_heads, nseq);
+    dim3 block(DT);
     const int esz = kind == KV_F32 ? 4 : 2;
     const int va = (kind == KV_T16 || kind == KV_TQ8) ? 16 : (((long)a.cap * esz) % 16 == 0 ? 16 : 8);
 #define L(HD, KIND, VA)                                                                        \
