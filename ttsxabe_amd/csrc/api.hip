@@ -259,6 +259,11 @@ void plan_decode(size_t tk_max, size_t units, size_t group, int& nit, int& split
     size_t per_wg = (blocks + want - 1) / want;           // 32-key blocks per workgroup
     size_t n = std::max<size_t>(1, (per_wg + 3) / 4);     // per wave
     if (const char* e = getenv("LLMTIE_DECODE_NIT")) n = std::max(1, atoi(e));
+    // A short context is one split: the cross-workgroup merge (three memory
+    // round trips, ~3 us) costs more than the extra parallelism saves below
+    // ~12 blocks per head (measured: 224 keys 9.2 us unsplit vs 12.4 us in
+    // two splits; 512 keys 10.7 us unsplit vs 10.0 us in two).
+    if (blocks <= 12 && !getenv("LLMTIE_DECODE_WGS") && !getenv("LLMTIE_DECODE_NIT")) n = (blocks + 3) / 4;
     size_t span = 4 * n * 32;
     while ((tk_max + span - 1) / span > max_splits) {
         ++n;
