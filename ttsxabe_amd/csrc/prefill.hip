@@ -459,17 +459,29 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     };
 
     // Q as B operands: qb[u][s] holds dims 32s + 8grp + 0..7 of query p0 + 16u + col.
+    // The first tile's loads go out before the query's (the query's first
+    // use waits for every load issued before it, tile loads included: the
+    // compiler does not count LDS-DMA loads in order).
+    if (kend > 0) issue(0, t0);
     const float qsc = a.scale_q ? a.scale : 1.0f;
-    half8 qb[NQT][NS];
+    float4 qx[NQT][NS][2];
 #pragma unroll
     for (int u = 0; u < NQT; ++u) {
         const int r = min(p0 + 16 * u + col, a.tq - 1);
-        const bool ok = p0 + 16 * u + col < a.tq;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const float4* p = reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 32 * s + 8 * grp);
-            const float4 x0 = p[0], x1 = p[1];
-            const float m = ok ? qsc : 0.0f;
+            qx[u][s][0] = p[0];
+            qx[u][s][1] = p[1];
+        }
+    }
+    half8 qb[NQT][NS];
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        const float m = p0 + 16 * u + col < a.tq ? qsc : 0.0f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const float4 x0 = qx[u][s][0], x1 = qx[u][s][1];
             half8 x;
             x[0] = to_h(x0.x * m); x[1] = to_h(x0.y * m); x[2] = to_h(x0.z * m); x[3] = to_h(x0.w * m);
             x[4] = to_h(x1.x * m); x[5] = to_h(x1.y * m); x[6] = to_h(x1.z * m); x[7] = to_h(x1.w * m);
@@ -626,7 +638,6 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
             tile(cur, kv0, std::false_type{});
     };
 
-    if (kend > 0) issue(0, t0);
     for (int kv0 = 0; kv0 < kend; kv0 += 2 * KT) {
         step(t0, t1, kv0);
         if (kv0 + KT < kend) step(t1, t0, kv0 + KT);
