@@ -633,7 +633,11 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const int nf = nfull > first ? min(nit, (nfull - first + DW - 1) / DW) : 0;
     const bool tail = (tk & 31) && nfull >= first && (nfull - first) % DW == 0 && (nfull - first) / DW < nit;
     Frag<HD, KIND> f0, f1;
+    // The first two blocks go out before the queries are read: the queries'
+    // first use waits for every load issued before them, so a block issued
+    // after that would start a second memory round trip.
     if (nf > 0) load_block<HD, KIND, VA, true>(c, first * 32, lane, f0);
+    if (nf > 1) load_block<HD, KIND, VA, true>(c, (first + DW) * 32, lane, f1);
 
     // The group's queries as B operands, hi + lo (columns past the group are
     // read from column 0 and zeroed, so every load is unconditional). The
@@ -681,25 +685,34 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
 #pragma unroll
     for (int t = 0; t < NT; ++t) o[t] = zero_f4();
 
-    // Every prefetch is unconditional (a block past this wave's last is
-    // clamped to its last and simply re-read): the wait counter then stands
-    // at the same count on every path into a fold, so each fold waits only
-    // for its own block. The scheduling barriers keep each prefetch ahead of
-    // the fold it is meant to overlap (left alone, the scheduler sinks loads
-    // towards their uses).
-    for (int i = 0; i < nf; i += 2) {
+    // Two blocks in flight: while block i is folded, block i + 1 is on its
+    // way. Inside the loop every prefetch is unconditional (a block past this
+    // wave's last is clamped to its last and re-read, at most once per wave
+    // and only for an odd block count), so the wait counter stands at the
+    // same count on every path into a fold and each fold waits only for its
+    // own block. The scheduling barriers keep each prefetch ahead of the fold
+    // it is meant to overlap (left alone, the scheduler sinks loads towards
+    // their uses).
+    int i = 0;
+    for (; i + 2 < nf; i += 2) {
         const int p0 = (first + i * DW) * 32;
-        const int p1 = (first + min(i + 1, nf - 1) * DW) * 32;
-        const int p2 = (first + min(i + 2, nf - 1) * DW) * 32;
-        load_block<HD, KIND, VA, true>(c, p1, lane, f1);
-        __builtin_amdgcn_sched_barrier(0);
+        const int p1 = (first + (i + 1) * DW) * 32;
+        const int p2 = (first + (i + 2) * DW) * 32;
+        const int p3 = (first + min(i + 3, nf - 1) * DW) * 32;
         fold_block<HD, KIND, false>(f0, qh, ql, qbias, p0, tk, grp, a.score_l2, m_run, l_run, o);
         __builtin_amdgcn_sched_barrier(0);
         load_block<HD, KIND, VA, true>(c, p2, lane, f0);
         __builtin_amdgcn_sched_barrier(0);
-        if (i + 1 < nf) fold_block<HD, KIND, false>(f1, qh, ql, qbias, p1, tk, grp, a.score_l2, m_run, l_run, o);
+        fold_block<HD, KIND, false>(f1, qh, ql, qbias, p1, tk, grp, a.score_l2, m_run, l_run, o);
+        __builtin_amdgcn_sched_barrier(0);
+        load_block<HD, KIND, VA, true>(c, p3, lane, f1);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // The last one or two blocks (already in f0, f1).
+    if (i < nf) fold_block<HD, KIND, false>(f0, qh, ql, qbias, (first + i * DW) * 32, tk, grp, a.score_l2, m_run, l_run, o);
+    if (i + 1 < nf)
+        fold_block<HD, KIND, false>(f1, qh, ql, qbias, (first + (i + 1) * DW) * 32, tk, grp, a.score_l2, m_run, l_run,
+                                    o);
     if (tail) {
         load_block<HD, KIND, VA, TILED>(c, nfull * 32, lane, f0);
         fold_block<HD, KIND, true>(f0, qh, ql, qbias, nfull * 32, tk, grp, a.score_l2, m_run, l_run, o);
