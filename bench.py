@@ -284,7 +284,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU (--gpus > 1) is out of scope: attention "
-                                   "shards by head/sequence with no exchange, see DESIGN.md"}))
+                                   "shards by kv head and sequence with no exchange inside attention"}))
         sys.exit(2)
     import torch
     if a.copy_calibration:
