@@ -7,11 +7,12 @@ The reference's own end-to-end check is the chat model's argmax against a
 captured run of the original (crates/llmtie-chat/tests/stepwise.rs); with no
 checkpoint here, the same check runs on random weights. The prompt is 250
 tokens so decoding crosses the 256-position cache capacity and exercises the
-growth path. Tolerances: the GPU rounds q and the probabilities to f16 in the
-prefill (the reference's flash arithmetic), so logits agree to ~1e-3 of their
-scale, not bit for bit; the GPU's argmax must be one of the CPU's near-ties
-within twice the measured logit error, and both sides continue from the CPU's
-token so one near-tie cannot cascade.
+growth path. The GPU rounds q and the probabilities to f16 in the prefill
+(the reference's flash arithmetic), so logits agree to ~1e-3 of their scale,
+not bit for bit. The argmax must be identical at every step whose CPU top-two
+margin exceeds twice the measured logit error; a step inside that margin is a
+numerical tie, where the GPU's choice must still be a CPU near-tie. Both
+sides continue from the CPU's token, so a tie cannot cascade.
 """
 import numpy as np
 import pytest
@@ -32,7 +33,7 @@ def test_random_llama_stack_decodes_like_the_cpu(gpu, layout):
     dev = LlamaStack(gpu, cfg, w, layout)
     rng = np.random.default_rng(SEED + 1)
     ids = [int(t) for t in rng.integers(0, cfg.vocab, 250)]
-    exact = 0
+    ties = 0
     for step in range(12):
         lc = cpu.forward(ids)
         lg = dev.forward(ids).float().cpu().numpy()
@@ -40,8 +41,14 @@ def test_random_llama_stack_decodes_like_the_cpu(gpu, layout):
         err = float(np.abs(lc - lg).max())
         assert err < 5e-3 * scale, f"{layout} step {step}: logit error {err:.3g} of scale {scale:.3g}"
         top_c, top_g = int(lc.argmax()), int(lg.argmax())
-        assert lc[top_g] >= lc[top_c] - 2 * err - 1e-6, f"{layout} step {step}: GPU argmax {top_g} is no CPU near-tie"
-        exact += top_c == top_g
+        srt = np.sort(lc)
+        margin = float(srt[-1] - srt[-2])
+        if margin > 2 * err + 1e-6:
+            # not a numerical tie: the argmax must be identical
+            assert top_g == top_c, f"{layout} step {step}: GPU argmax {top_g} != CPU {top_c} (margin {margin:.3g})"
+        else:
+            assert lc[top_g] >= lc[top_c] - 2 * err - 1e-6, f"{layout} step {step}: {top_g} is no CPU near-tie"
+            ties += 1
         ids = [top_c]
     assert dev.past == cpu.past == 261 and dev.cap == 512
-    assert exact >= 10, f"{layout}: only {exact} of 12 argmaxes equal"
+    assert ties <= 2, f"{layout}: {ties} of 12 steps were numerical ties (random weights should rarely tie)"
