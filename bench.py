@@ -250,10 +250,24 @@ def cpu_baseline(seconds: float):
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    return dict(value=round(bytes_layer * n / el / 1e9, 4), unit="GB/s", cores=1, kind="port",
-                sample=f"{n} C2 decode layer-steps (32/8/128 GQA, 4096-position f16 cache) through the oracle's "
-                       f"scalar f32 chain, 1 thread, {el:.1f} s",
-                ms_per_layer_step=round(el / n * 1e3, 2))
+    out = dict(value=round(bytes_layer * n / el / 1e9, 4), unit="GB/s", cores=1, kind="port",
+               sample=f"{n} C2 decode layer-steps (32/8/128 GQA, 4096-position f16 cache) through the oracle's "
+                      f"scalar f32 chain, 1 thread, {el:.1f} s",
+               ms_per_layer_step=round(el / n * 1e3, 2))
+    # The same chain with the query heads spread over the host's cores
+    # (OpenMP), about a fifth of the time budget.
+    threads = min(heads, os.cpu_count() or 1)
+    if oracle.has_openmp() and threads > 1:
+        n2, t0 = 0, time.perf_counter()
+        while True:
+            oracle.decode_f16(q, k, v, heads, kv, hd, tk, tk, hd ** -0.5, False, threads=threads)
+            n2 += 1
+            el2 = time.perf_counter() - t0
+            if el2 >= seconds / 5:
+                break
+        out["all_cores"] = dict(value=round(bytes_layer * n2 / el2 / 1e9, 4), unit="GB/s", threads=threads,
+                                ms_per_layer_step=round(el2 / n2 * 1e3, 2))
+    return out
 
 
 def cpu_c1(seconds=3.0):
