@@ -102,3 +102,49 @@ def test_q8_refusals(gpu):
     from ttsxabe_amd.gpu import SliceOverrun
     with pytest.raises(SliceOverrun):
         gpu.attn_decode_q8_batch(q, short, tk, tk * 0, 10, 8, 0.1, False, s)
+
+
+def check_batch(gpu, hd, heads, kv, slots, cap, tk, slot, seed, scale_q=False):
+    """The batched decode of (tk, slot) against the exact f64 attention on
+    the dequantised cache, and bit-identical on a repeated call."""
+    from ttsxabe_amd.gpu import DecodeScratch, KvCacheQ8
+    kc, ks, vc, vs = random_q8_cache(slots, kv, hd, cap, seed)
+    cache = KvCacheQ8(slots, kv, hd, cap)
+    load(cache, kc, ks, vc, vs)
+    nseq = len(tk)
+    q = oracle.normal(nseq * heads * hd, seed + 7)
+    scale = hd ** -0.5
+    s = DecodeScratch()
+    max_tk = int(max(tk))
+    call = lambda: down(gpu.attn_decode_q8_batch(up(q), cache, up(tk, torch.int32), up(slot, torch.int32), max_tk,
+                                                 heads, scale, scale_q, s))
+    got = call()
+    assert np.array_equal(got, call())
+    n = heads * hd
+    for i in range(nseq):
+        k, v = dequant_seq(kc, ks, vc, vs, slot[i], kv, hd, cap)
+        exact = oracle.decode_f64(q[i * n:(i + 1) * n], k, v, heads, kv, hd, int(tk[i]), cap, scale, scale_q)
+        assert full_scale_err(exact, got[i * n:(i + 1) * n]) < 1e-3, f"seq {i} (tk {tk[i]})"
+
+
+def test_many_one_block_heads(gpu):
+    """64 sequences of 1..40 keys: every wave's range holds many whole heads
+    and segments that begin while another segment's queries are pending."""
+    tk = (oracle.uniform_int(64, 31, 1, 40)).astype(np.int32)
+    check_batch(gpu, 128, 32, 8, 64, 64, tk, np.arange(64, dtype=np.int32)[::-1].copy(), 40)
+
+
+def test_one_long_sequence_many_contributors(gpu):
+    """One sequence of 8191 keys: every head is shared by more waves than one
+    merge batch holds."""
+    check_batch(gpu, 128, 32, 8, 1, 8192, np.array([8191], np.int32), np.array([0], np.int32), 41)
+
+
+def test_ragged_mix_and_head_width_64(gpu):
+    tk = (oracle.uniform_int(33, 32, 1, 3000)).astype(np.int32)
+    check_batch(gpu, 64, 16, 4, 33, 3008, tk, np.arange(33, dtype=np.int32), 42, scale_q=True)
+
+
+def test_more_than_64_sequences_take_the_planned_grid(gpu):
+    tk = (oracle.uniform_int(70, 33, 1, 300)).astype(np.int32)
+    check_batch(gpu, 128, 8, 2, 70, 320, tk, np.arange(70, dtype=np.int32), 43)

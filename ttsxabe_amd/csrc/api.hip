@@ -359,7 +359,7 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     plan_decode(tk, kv_heads, group, nit, splits);
     const size_t part = kv_heads * (size_t)splits * group * (hd + 2);
     const long ml_off = (long)(kv_heads * (size_t)splits * group * hd);
-    int r = ensure_scratch(scratch, part, kv_heads, S(stream));
+    int r = ensure_scratch(scratch, part, kv_heads * CTR_STRIDE, S(stream));
     if (r != LLMTIE_OK) return r;
     DecodeArgs a;
     memset(&a, 0, sizeof a);
@@ -495,25 +495,19 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     const size_t group = heads / kv_heads;
     int nit, splits;
     plan_decode(max_tk, kv_heads * nseq, group, nit, splits);
-    // Up to 64 sequences are planned on the device from their real lengths
-    // (the host knows only max_tk): a 1-D grid of two workgroups per compute
-    // unit, every one resident at once, each running one equal-sized item.
-    const bool dyn = nseq <= 64 && !getenv("LLMTIE_DECODE_STATIC");
-    int nit_max = 0, items = 0;
-    if (dyn) {
-        const size_t max_splits =
-            std::min<size_t>(DECODE_MAX_SPLITS, DECODE_MAX_SPLIT_ROWS / std::max<size_t>(1, group));
-        nit = 1;  // smallest blocks-per-wave whose splits the merge can hold
-        while ((max_tk + 128 * (size_t)nit - 1) / (128 * (size_t)nit) > max_splits) ++nit;
-        nit_max = (int)std::max<size_t>((size_t)nit, (max_tk + 127) / 128);
-        splits = (int)((max_tk + 128 * (size_t)nit - 1) / (128 * (size_t)nit));
-        int per_cu = 2;
-        if (const char* e = getenv("LLMTIE_DECODE_ITEMS_PER_CU")) per_cu = std::max(1, atoi(e));
-        items = std::max(per_cu * compute_units(), (int)(kv_heads * nseq));
+    // Up to 64 sequences go through the stream-K kernel, one workgroup per
+    // compute unit, each wave an equal share of the batch's blocks; a larger
+    // batch through the host-planned grid (splits of the longest sequence).
+    const bool sk = nseq <= 64 && !getenv("LLMTIE_DECODE_STATIC");
+    const int items = sk ? compute_units() : 0;
+    size_t part = nseq * kv_heads * (size_t)splits * group * (head_dim + 2);
+    long ml_off = (long)(nseq * kv_heads * (size_t)splits * group * head_dim);
+    if (sk) {
+        const size_t slots2 = (size_t)items * 4 * 2;
+        ml_off = (long)(slots2 * 16 * head_dim);
+        part = slots2 * (16 * head_dim + 32);
     }
-    const size_t part = nseq * kv_heads * (size_t)splits * group * (head_dim + 2);
-    const long ml_off = (long)(nseq * kv_heads * (size_t)splits * group * head_dim);
-    int r = ensure_scratch(scratch, part, nseq * kv_heads, S(stream));
+    int r = ensure_scratch(scratch, part, nseq * kv_heads * CTR_STRIDE, S(stream));
     if (r != LLMTIE_OK) return r;
     DecodeArgs a;
     memset(&a, 0, sizeof a);
@@ -536,15 +530,10 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     a.qscale = scale_q ? scale : 1.0f;
     a.nit = nit;
     a.splits = splits;
-    // A device-planned batch merges in-launch (measured faster at C5 than a
-    // second launch: each head has few splits, and its last arriver merges
-    // while the rest of the batch still streams).
-    a.two_phase = dyn ? (getenv("LLMTIE_DECODE_TWO_PHASE") ? two_phase_merge(items, 1) : 0)
-                      : two_phase_merge(splits, kv_heads * nseq);
-    a.dyn = dyn ? 1 : 0;
+    a.two_phase = sk ? 0 : two_phase_merge(splits, kv_heads * nseq);
+    a.sk = sk ? 1 : 0;
     a.nseq = (int)nseq;
     a.items = items;
-    a.nit_max = nit_max;
     return launched("attn_decode_q8_batch", launch_decode((int)head_dim, KV_TQ8, a, (int)kv_heads, (int)nseq, S(stream)));
 }
 

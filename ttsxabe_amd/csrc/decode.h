@@ -12,6 +12,10 @@ enum KvKind { KV_F16 = 0, KV_F32 = 1, KV_T16 = 2, KV_TQ8 = 3 };
 constexpr int DECODE_MAX_SPLITS = 256;
 constexpr int DECODE_MAX_SPLIT_ROWS = 1024;
 
+// Arrival counters sit a 256-byte line apart: counters sharing a line
+// serialise every workgroup's atomic at one memory channel.
+constexpr int CTR_STRIDE = 64;
+
 struct DecodeArgs {
     const float* q;          // query rows, f32
     const void* k;           // K values (reference layouts) or the tiled block array
@@ -21,7 +25,7 @@ struct DecodeArgs {
     float* twin_scales;      // its per-32 scales
     float* part;             // split partials: O area, then the (m, l) area at ml_off
     long ml_off;             // floats from part to the (m, l) area
-    unsigned* ctr;           // one arrival counter per (sequence, kv head), zero between calls
+    unsigned* ctr;           // arrival counters, one per (sequence, kv head) every CTR_STRIDE words, zero between calls
     const int* tk_arr;       // per-sequence live lengths (batched) or null
     const int* slot_arr;     // per-sequence cache slot (batched) or null
     long q_off, q_stride;    // element offset of sequence 0's query; elements per sequence
@@ -36,13 +40,11 @@ struct DecodeArgs {
     int nit;                 // 32-key blocks per wave per split
     int splits;              // grid.x: splits of the longest sequence
     int two_phase;           // merge in a second launch (else the last split's workgroup merges)
-    // Batched sequences planned on the device (dyn != 0): the launch is a 1-D
-    // grid of `items` workgroups; every workgroup reads the batch's lengths,
-    // takes the smallest blocks-per-wave in [nit, nit_max] whose work items
-    // (kv heads x splits of every sequence) fit in `items`, and runs the item
-    // its index names (sequence-major, then split, then kv head). `splits`
-    // is then the largest split count any plan can give (the scratch stride).
-    int dyn, nseq, items, nit_max;
+    // Stream-K batch (sk != 0, Q8_0 cache, nseq <= 64): a 1-D grid of
+    // `items` workgroups whose waves each take an equal range of the batch's
+    // (sequence, kv head, 32-key block) list. Partial slots: two per wave, O
+    // [16][hd] floats each, then the (m, l) area at ml_off, 32 floats each.
+    int sk, nseq, items;
 };
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);

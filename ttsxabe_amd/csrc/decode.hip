@@ -265,7 +265,7 @@ __device__ __forceinline__ half_t h_at(const uint4& u, int e) {
 // >= tk are dropped (only the partial block needs it).
 template <int HD, int KIND, bool MASK>
 __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 (&qh)[HD / 32],
-                                           const half8 (&ql)[HD / 32], const floatx4 (&qbias)[HD / 32],
+                                           const half8 (&ql)[HD / 32],
                                            int p0, int tk, int grp,
                                            float score_l2, float& m_run, float& l_run,
                                            floatx4 (&o)[HD / 16]) {
@@ -285,11 +285,13 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
                 acc = mfma16(f.kh[T][s], ql[s], acc);
                 acc = mfma16(f.kl[T][s], qh[s], acc);
             } else {
-                // K enters biased (1152 + code); the accumulator starts at
-                // -1152 * sum(q over the block's 32 dims), which removes it.
+                // K enters as exact f16 codes (the 1152 offset taken off
+                // before the product: left in, it would cancel against the f32
+                // accumulator and cost ~1e-3 of score precision), scaled per
+                // dim block after the product.
                 const uint4& w = f.kc[T][s >> 1];
-                const half8 kq = (s & 1) ? dq8_biased(w.z, w.w) : dq8_biased(w.x, w.y);
-                floatx4 b = mfma16(kq, qh[s], qbias[s]);
+                const half8 kq = (s & 1) ? dq8(w.z, w.w) : dq8(w.x, w.y);
+                floatx4 b = mfma16(kq, qh[s], zero_f4());
                 b = mfma16(kq, ql[s], b);
                 // Key 8g + 4T + r, dim block s: half 4T + r of the block's scale piece.
 #pragma unroll
@@ -310,10 +312,14 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
     const float mn = fmaxf(m_run, mx);
     const float fac = ex2(m_run - mn);
     m_run = mn;
+    // Q8_0: probabilities carry a factor 2^10 (in l and O alike, so O / l is
+    // unchanged), which keeps P' = P * d_v (d_v ~ 1e-2) clear of the f16
+    // subnormal range where its relative precision would fall away.
+    const float mb = KIND == KV_TQ8 ? mn - 10.0f : mn;
     float p[8], ps = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        p[j] = ex2(sc[j] - mn);
+        p[j] = ex2(sc[j] - mb);
         ps += p[j];
     }
     l_run = l_run * fac + ps;
@@ -530,35 +536,6 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
 }
 
 
-// Device-side plan of a batched launch (DecodeArgs::dyn). Lane l of the wave
-// holds sequence l's effective length (nseq <= 64): its live length, clamped
-// to the launch bound, or 1 for a sequence the batch describes wrongly (it
-// still gets one item, to write its NaN row).
-__device__ __forceinline__ int dyn_len(const DecodeArgs& a, int lane) {
-    if (lane >= a.nseq) return 0;
-    const int tk = min(a.tk_arr[lane], a.tk);
-    const int slot = a.slot_arr[lane];
-    return (slot < 0 || slot >= a.slots || tk <= 0) ? 1 : tk;
-}
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-// Smallest blocks-per-wave n in [a.nit, a.nit_max] with kv x sum of
-// ceil(len / span(n)) <= a.items (the host guarantees it holds at nit_max).
-__device__ __forceinline__ int dyn_nit(const DecodeArgs& a, int len, int nw) {
-    int lo = a.nit, hi = a.nit_max;
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        const int span = nw * mid * 32;
-        const int items = a.kv_heads * wave_sum(len > 0 ? (len + span - 1) / span : 0);
-        if (items <= a.items) hi = mid;
-        else lo = mid + 1;
-    }
-    return lo;
-}
-
 template <int HD, int KIND, int VA>
 __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel(DecodeArgs a) {
     constexpr int NS = HD / 32;
@@ -572,28 +549,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
-    int split = blockIdx.x, h = blockIdx.y, seq = blockIdx.z, nit = a.nit;
-    if (a.dyn) {
-        const int len = dyn_len(a, lane);
-        nit = dyn_nit(a, len, DW);
-        const int span = DW * nit * 32;
-        // This workgroup's item: sequence-major prefix sums of kv x splits.
-        const int cnt = len > 0 ? a.kv_heads * ((len + span - 1) / span) : 0;
-        int incl = cnt;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
-        const int item = blockIdx.x;
-        const unsigned long long past = __ballot(incl <= item);  // sequences wholly before the item
-        seq = __popcll(past);
-        if (seq >= a.nseq) return;  // a spare workgroup: the plan needs fewer items
-        const int before = __shfl(incl - cnt, seq, 64);
-        const int r = item - before;
-        split = r / a.kv_heads;
-        h = r % a.kv_heads;
-    }
+    const int split = blockIdx.x, h = blockIdx.y, seq = blockIdx.z, nit = a.nit;
     const int group = a.group;
     const int tk = a.tk_arr ? min(a.tk_arr[seq], a.tk) : a.tk;
     const int slot = a.slot_arr ? a.slot_arr[seq] : 0;
@@ -666,20 +622,6 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         }
     }
 
-    // -1152 * (the block-s dims of q summed), per query column: the
-    // accumulator start that cancels the offset of biased Q8_0 K codes.
-    floatx4 qbias[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        float t = 0.0f;
-        if constexpr (KIND == KV_TQ8) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) t += (float)qh[s][j] + (float)ql[s][j];
-            t = -1152.0f * sum4grp(t);
-        }
-        qbias[s] = floatx4{t, t, t, t};
-    }
-
     float m_run = ninf(), l_run = 0.0f;
     floatx4 o[NT];
 #pragma unroll
@@ -699,23 +641,23 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         const int p1 = (first + (i + 1) * DW) * 32;
         const int p2 = (first + (i + 2) * DW) * 32;
         const int p3 = (first + min(i + 3, nf - 1) * DW) * 32;
-        fold_block<HD, KIND, false>(f0, qh, ql, qbias, p0, tk, grp, a.score_l2, m_run, l_run, o);
+        fold_block<HD, KIND, false>(f0, qh, ql, p0, tk, grp, a.score_l2, m_run, l_run, o);
         __builtin_amdgcn_sched_barrier(0);
         load_block<HD, KIND, VA, true>(c, p2, lane, f0);
         __builtin_amdgcn_sched_barrier(0);
-        fold_block<HD, KIND, false>(f1, qh, ql, qbias, p1, tk, grp, a.score_l2, m_run, l_run, o);
+        fold_block<HD, KIND, false>(f1, qh, ql, p1, tk, grp, a.score_l2, m_run, l_run, o);
         __builtin_amdgcn_sched_barrier(0);
         load_block<HD, KIND, VA, true>(c, p3, lane, f1);
         __builtin_amdgcn_sched_barrier(0);
     }
     // The last one or two blocks (already in f0, f1).
-    if (i < nf) fold_block<HD, KIND, false>(f0, qh, ql, qbias, (first + i * DW) * 32, tk, grp, a.score_l2, m_run, l_run, o);
+    if (i < nf) fold_block<HD, KIND, false>(f0, qh, ql, (first + i * DW) * 32, tk, grp, a.score_l2, m_run, l_run, o);
     if (i + 1 < nf)
-        fold_block<HD, KIND, false>(f1, qh, ql, qbias, (first + (i + 1) * DW) * 32, tk, grp, a.score_l2, m_run, l_run,
+        fold_block<HD, KIND, false>(f1, qh, ql, (first + (i + 1) * DW) * 32, tk, grp, a.score_l2, m_run, l_run,
                                     o);
     if (tail) {
         load_block<HD, KIND, VA, TILED>(c, nfull * 32, lane, f0);
-        fold_block<HD, KIND, true>(f0, qh, ql, qbias, nfull * 32, tk, grp, a.score_l2, m_run, l_run, o);
+        fold_block<HD, KIND, true>(f0, qh, ql, nfull * 32, tk, grp, a.score_l2, m_run, l_run, o);
     }
     l_run = sum4grp(l_run);
 
@@ -822,7 +764,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    unsigned* ctr = a.ctr + head;
+    unsigned* ctr = a.ctr + head * CTR_STRIDE;
     if (tid == 0) {
         const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = prev == (unsigned)(nsplit - 1);
@@ -845,7 +787,7 @@ __global__ __launch_bounds__(DT) void attn_merge_kernel(DecodeArgs a) {
     const int tk = a.tk_arr ? min(a.tk_arr[seq], a.tk) : a.tk;
     const int slot = a.slot_arr ? a.slot_arr[seq] : 0;
     if (a.slot_arr && (slot < 0 || slot >= a.slots || tk <= 0)) return;
-    const int nit = a.dyn ? dyn_nit(a, dyn_len(a, threadIdx.x & 63), DW) : a.nit;
+    const int nit = a.nit;
     const int span = DW * nit * 32;
     const int nsplit = (tk + span - 1) / span;
     if (nsplit <= 1) return;  // the attention launch wrote this head itself
@@ -864,11 +806,484 @@ __global__ __launch_bounds__(DT) void attn_merge_kernel(DecodeArgs a) {
     merge_head<HD, false>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
 }
 
+// ------------------------------------------------------------------------
+// Stream-K batched decode over a tiled cache (the device-planned batch).
+//
+// Every (sequence, kv head, 32-key block) of the batch is one position of a
+// flat list, sequence-major, then kv head, then block; the launch's waves
+// each take an equal contiguous range of it, so every wave streams the same
+// number of blocks whatever the spread of the sequences' lengths (a
+// per-head split of a fixed span leaves the last, short split of each head
+// idle for most of the launch). A wave walks its range with the two-deep
+// block prefetch of attn_decode_kernel; the range falls into segments, one
+// per kv head it touches:
+//   - a segment that is a whole head: the wave normalises and writes the
+//     context rows itself;
+//   - a segment that is part of a head (at most the first and the last of
+//     the range): the wave publishes (m, l, O) to its own partial slot
+//     (slot 0: a segment ending before the range does; slot 1: the one
+//     ending with it) and, after its range, counts its arrival at the head;
+//     the last arriver merges the head's partials in range order.
+// A segment's queries are moved into LDS by a direct-to-LDS load issued just
+// before its first block's loads, so they arrive with that block and cost
+// no registers while in flight.
+
+// Lane l's value as a wave-uniform (scalar) one: l must be uniform.
+__device__ __forceinline__ int rdlane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ long rdlane64(long v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((unsigned long)v >> 32), l);
+    return (long)(((unsigned long)hi << 32) | lo);
+}
+
+// Waves of the launch that take part (never more than there are blocks, so
+// every wave's range is non-empty), and wave u's range [first(u), first(u+1)).
+__device__ __forceinline__ long sk_first(long u, long nw, long total) { return u * total / nw; }
+// The wave whose range holds position p.
+__device__ __forceinline__ long sk_owner(long p, long nw, long total) { return ((p + 1) * nw - 1) / total; }
+
+// The batch's sequences, one per lane (nseq <= 64): blocks per kv head and
+// the position of the sequence's first block in the flat list.
+struct SkSeqs {
+    int nb;      // 32-key blocks per kv head (0: a sequence the batch describes wrongly)
+    int tk, slot;
+    long base;   // flat position of (this sequence, kv head 0, block 0)
+    long total;  // positions in the whole batch (wave-uniform)
+};
+__device__ __forceinline__ SkSeqs sk_seqs(const DecodeArgs& a, int lane) {
+    SkSeqs q;
+    q.tk = 0;
+    q.slot = 0;
+    q.nb = 0;
+    if (lane < a.nseq) {
+        q.tk = min(a.tk_arr[lane], a.tk);
+        q.slot = a.slot_arr[lane];
+        if (q.slot >= 0 && q.slot < a.slots && q.tk > 0) q.nb = (q.tk + 31) >> 5;
+    }
+    const long cnt = (long)q.nb * a.kv_heads;
+    long incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const long y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    q.base = incl - cnt;
+    q.total = rdlane64(incl, 63);
+    return q;
+}
+
+// Where flat position p lies: sequence, kv head, block (all wave-uniform).
+struct SkPos {
+    int s, h, blk, nb, tk, slot;
+};
+__device__ __forceinline__ SkPos sk_locate(const SkSeqs& q, long p, int kv_heads) {
+    // Sequences whose blocks all lie before p (a prefix of the lanes: lanes
+    // past the batch have base = total > p).
+    const int s = __popcll(__ballot(q.base + (long)q.nb * kv_heads <= p));
+    SkPos r;
+    r.s = s;
+    r.nb = rdlane(q.nb, s);
+    r.tk = rdlane(q.tk, s);
+    r.slot = rdlane(q.slot, s);
+    const long off = p - rdlane64(q.base, s);
+    r.h = (int)(off / r.nb);
+    r.blk = (int)(off % r.nb);
+    return r;
+}
+
+// s_waitcnt with only the vector-memory count bounded (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// The LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// One tiled Q8_0 block from LDS (at byte address b) into a fragment set, as
+// one asm block that also waits for its own reads. The compiler cannot tell
+// which direct-to-LDS load wrote which bytes, so before an LDS read it knows
+// of it waits for every outstanding load, the next block's prefetch
+// included; this read is ordered by the caller's explicit vmcnt wait instead.
+template <int HD>
+__device__ __forceinline__ void ring_read(uint32_t b, int lane, int grp, Frag<HD, KV_TQ8>& f);
+template <>
+__device__ __forceinline__ void ring_read<128>(uint32_t b, int lane, int grp, Frag<128, KV_TQ8>& f) {
+    // codes: K (T, sp) at ((T*2 + sp)*64 + lane)*16, V tile pair tp at 4096 + (tp*64 + lane)*16;
+    // scales: K dim block i at 8192 + (i*4 + grp)*16, V at 8192 + 256 + ...
+    const uint32_t c = b + 16 * lane, sc = b + 8192 + 16 * grp;
+    asm volatile(
+        "ds_read_b128 %0, %16\n"
+        "ds_read_b128 %1, %16 offset:1024\n"
+        "ds_read_b128 %2, %16 offset:2048\n"
+        "ds_read_b128 %3, %16 offset:3072\n"
+        "ds_read_b128 %4, %16 offset:4096\n"
+        "ds_read_b128 %5, %16 offset:5120\n"
+        "ds_read_b128 %6, %16 offset:6144\n"
+        "ds_read_b128 %7, %16 offset:7168\n"
+        "ds_read_b128 %8, %17\n"
+        "ds_read_b128 %9, %17 offset:64\n"
+        "ds_read_b128 %10, %17 offset:128\n"
+        "ds_read_b128 %11, %17 offset:192\n"
+        "ds_read_b128 %12, %17 offset:256\n"
+        "ds_read_b128 %13, %17 offset:320\n"
+        "ds_read_b128 %14, %17 offset:384\n"
+        "ds_read_b128 %15, %17 offset:448\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=v"(f.kc[0][0]), "=v"(f.kc[0][1]), "=v"(f.kc[1][0]), "=v"(f.kc[1][1]), "=v"(f.vc[0]), "=v"(f.vc[1]),
+          "=v"(f.vc[2]), "=v"(f.vc[3]), "=v"(f.ks[0]), "=v"(f.ks[1]), "=v"(f.ks[2]), "=v"(f.ks[3]), "=v"(f.vs[0]),
+          "=v"(f.vs[1]), "=v"(f.vs[2]), "=v"(f.vs[3])
+        : "v"(c), "v"(sc));
+}
+template <>
+__device__ __forceinline__ void ring_read<64>(uint32_t b, int lane, int grp, Frag<64, KV_TQ8>& f) {
+    // codes: K (T, 0) at (T*64 + lane)*16, V tile pair tp at 2048 + (tp*64 + lane)*16;
+    // scales: K dim block i at 4096 + (i*4 + grp)*16, V at 4096 + 128 + ...
+    const uint32_t c = b + 16 * lane, sc = b + 4096 + 16 * grp;
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:1024\n"
+        "ds_read_b128 %2, %8 offset:2048\n"
+        "ds_read_b128 %3, %8 offset:3072\n"
+        "ds_read_b128 %4, %9\n"
+        "ds_read_b128 %5, %9 offset:64\n"
+        "ds_read_b128 %6, %9 offset:128\n"
+        "ds_read_b128 %7, %9 offset:192\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=v"(f.kc[0][0]), "=v"(f.kc[1][0]), "=v"(f.vc[0]), "=v"(f.vc[1]), "=v"(f.ks[0]), "=v"(f.ks[1]),
+          "=v"(f.vs[0]), "=v"(f.vs[1])
+        : "v"(c), "v"(sc));
+}
+
+// A lane's query operands from a raw [g][HD] f32 buffer in LDS (b = the
+// byte address of its column's dims 8*grp ..): dims 32s + 8grp + 0..7 as
+// two float4 per s, read as one asm block (see ring_read).
+template <int HD>
+__device__ __forceinline__ void q_read(uint32_t b, float4 (&x)[HD / 32][2]);
+template <>
+__device__ __forceinline__ void q_read<128>(uint32_t b, float4 (&x)[4][2]) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:16\n"
+        "ds_read_b128 %2, %8 offset:128\n"
+        "ds_read_b128 %3, %8 offset:144\n"
+        "ds_read_b128 %4, %8 offset:256\n"
+        "ds_read_b128 %5, %8 offset:272\n"
+        "ds_read_b128 %6, %8 offset:384\n"
+        "ds_read_b128 %7, %8 offset:400\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=v"(x[0][0]), "=v"(x[0][1]), "=v"(x[1][0]), "=v"(x[1][1]), "=v"(x[2][0]), "=v"(x[2][1]), "=v"(x[3][0]),
+          "=v"(x[3][1])
+        : "v"(b));
+}
+template <>
+__device__ __forceinline__ void q_read<64>(uint32_t b, float4 (&x)[2][2]) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n"
+        "ds_read_b128 %1, %4 offset:16\n"
+        "ds_read_b128 %2, %4 offset:128\n"
+        "ds_read_b128 %3, %4 offset:144\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=v"(x[0][0]), "=v"(x[0][1]), "=v"(x[1][0]), "=v"(x[1][1])
+        : "v"(b));
+}
+
+// The Q8_0 stream-K kernel. Each wave owns a two-slot ring of whole tiled
+// blocks in LDS, filled by direct-to-LDS loads (no registers held while a
+// block is in flight): fold i waits for slot i % 2, reads the block into
+// registers, refills the slot with block i + 2 and folds from registers, so
+// two blocks are always on their way. One workgroup per compute unit: at
+// two, 2048 concurrent streams measured slower (first data up to 17 us late,
+// and 256 VGPRs spill).
+template <int HD>
+__global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
+    constexpr int KIND = KV_TQ8;
+    constexpr int NS = HD / 32;
+    constexpr int NT = HD / 16;
+    constexpr int BB = (int)tq8_block_bytes(HD);  // bytes of one block
+    constexpr int CODE_I = 64 * HD / 1024;        // 1 KB code loads per block
+    constexpr int SCL_L = (BB - 64 * HD) / 16;    // lanes of the one scale load
+    constexpr int LPB = CODE_I + 1;               // load instructions per block
+    static_assert(SCL_L <= 64, "scales in one wave-wide load");
+    __shared__ __attribute__((aligned(16))) char ring[DW][2][BB];
+    // Dynamic: per wave, one raw query buffer of group * HD floats (the
+    // destination of a segment's direct-to-LDS query loads).
+    extern __shared__ __attribute__((aligned(16))) float sk_qraw[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int group = a.group, kv = a.kv_heads;
+    const int n = group * HD;           // context floats per (sequence, kv head)
+    const long heads_n = (long)kv * n;  // context floats per sequence
+
+    const SkSeqs sq = sk_seqs(a, lane);
+    const long total = sq.total;
+    const long nw = min((long)gridDim.x * DW, total);
+    const long u = (long)blockIdx.x * DW + wave;
+
+    // A sequence the batch describes wrongly gets a NaN row (written by the
+    // launch's first wave), never a read outside its cache.
+    if (u == 0) {
+        for (int s = 0; s < a.nseq; ++s) {
+            if (rdlane(sq.nb, s) == 0) {
+                float* o = a.out + a.out_off + (size_t)s * a.out_stride;
+                for (long e = lane; e < heads_n; e += 64) o[e] = __builtin_nanf("");
+            }
+        }
+    }
+    if (u >= nw) return;
+    const long p_first = sk_first(u, nw, total), p_end = sk_first(u + 1, nw, total);
+    const long nblk_cap = tiled_nblk(a.cap);
+
+    // The next block to issue, as a cursor stepping through the list
+    // (wave-uniform, no division per block).
+    SkPos ci = sk_locate(sq, p_first, kv);
+    auto step = [&](SkPos& r) {
+        if (++r.blk < r.nb) return;
+        r.blk = 0;
+        if (++r.h < kv) return;
+        r.h = 0;
+        do {
+            ++r.s;
+        } while (r.s < 63 && rdlane(sq.nb, r.s) == 0);
+        r.nb = rdlane(sq.nb, r.s);
+        r.tk = rdlane(sq.tk, r.s);
+        r.slot = rdlane(sq.slot, r.s);
+    };
+    // A segment's queries, raw f32 [g][HD], are moved into one of the wave's
+    // two LDS query buffers just before its first block's loads, so they
+    // land with that block. Segments take the buffers alternately, in issue
+    // order; by the time a third segment's queries are issued, the first's
+    // have been converted (a fold converts its segment's queries before it
+    // issues the block two ahead).
+    float* const qbufs = sk_qraw + (size_t)wave * 2 * n;
+    int q_in = 0, q_out = 0;  // the buffer the next segment's queries go to / come from
+    auto load_q = [&](const SkPos& r, int buf) {
+        const float* src = a.q + a.q_off + (size_t)r.s * a.q_stride + (size_t)r.h * n;
+        for (int i = 0; i < n; i += 256)
+            if (i + 4 * lane < n) __builtin_amdgcn_global_load_lds(src + i + 4 * lane, qbufs + buf * n + i, 16, 0, 0);
+    };
+    // Vector-memory instructions this wave has issued (loads and stores
+    // retire in issue order on this part), and the count just after each
+    // ring slot's block: a fold waits with vmcnt = everything issued since.
+    // Every instruction counted here is issued with lane 0 active.
+    int vm_ops = 0, mark[2] = {0, 0};
+    const int q_instr = (n + 255) / 256;
+    // Issues the block at the cursor into ring slot `slot` and returns where
+    // it lies; past the range's end nothing is issued. The first block of a
+    // segment is preceded by its queries' loads.
+    long pi = p_first;
+    auto issue = [&](int slot) {
+        const SkPos r = ci;
+        if (pi >= p_end) return r;
+        if (pi == p_first || r.blk == 0) {
+            load_q(r, q_in);
+            q_in ^= 1;
+            vm_ops += q_instr;
+        }
+        const char* src = reinterpret_cast<const char*>(a.k) +
+                          (((size_t)r.slot * kv + r.h) * nblk_cap + r.blk) * (size_t)BB;
+        char* dst = &ring[wave][slot][0];
+#pragma unroll
+        for (int i = 0; i < CODE_I; ++i)
+            __builtin_amdgcn_global_load_lds(src + 1024 * i + 16 * lane, dst + 1024 * i, 16, 0, 0);
+        if (lane < SCL_L)
+            __builtin_amdgcn_global_load_lds(src + 64 * HD + 16 * lane, dst + 64 * HD, 16, 0, 0);
+        vm_ops += LPB;
+        mark[slot] = vm_ops;
+        if (pi + 1 < p_end) step(ci);
+        ++pi;
+        return r;
+    };
+
+    half8 qh[NS], ql[NS];
+    float m_run = ninf(), l_run = 0.0f;
+    floatx4 o[NT];
+    // Pending partial publications (slot 0, slot 1): the head's flat start
+    // position, or -1.
+    long pend0 = -1, pend1 = -1;
+
+    SkPos r0 = issue(0);
+    SkPos r1 = issue(1);
+
+    // Fold of the block in ring slot `slot` at flat position pp; rn: the
+    // position of the block issued into the slot afterwards.
+    auto fold_at = [&](int slot, long pp, const SkPos r, SkPos& rn) {
+        // This block has landed once at most the instructions issued after
+        // its loads are outstanding.
+        // Rounded down to three levels (a smaller count only waits longer):
+        // nothing after it (the range's last block), the steady state (the
+        // next block's loads), and after a publish (its stores too).
+        const int after = __builtin_amdgcn_readfirstlane(vm_ops - (slot ? mark[1] : mark[0]));
+        if (after >= LPB + NT) wait_vm<LPB + NT>();
+        else if (after >= LPB) wait_vm<LPB>();
+        else wait_vm<0>();
+        Frag<HD, KIND> f;
+        ring_read<HD>(lds_addr(&ring[wave][slot][0]), lane, grp, f);
+        if (pp == p_first || r.blk == 0) {
+            // A new segment: its queries as hi + lo f16 B operands, scaled
+            // into log2 units.
+            const bool qok = col < group;
+            float4 x[NS][2];
+            q_read<HD>(lds_addr(qbufs + q_out * n) + 4 * ((qok ? col : 0) * HD + 8 * grp), x);
+            q_out ^= 1;
+            const float qs = qok ? a.qscale * a.score_l2 : 0.0f;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const float xs[8] = {x[s][0].x, x[s][0].y, x[s][0].z, x[s][0].w,
+                                     x[s][1].x, x[s][1].y, x[s][1].z, x[s][1].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    half_t hh, ll;
+                    split_h(xs[j] * qs, hh, ll);
+                    qh[s][j] = hh;
+                    ql[s][j] = ll;
+                }
+            }
+            m_run = ninf();
+            l_run = 0.0f;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[t] = zero_f4();
+        }
+        // The slot (and the query buffer) are read: refill the slot with the
+        // block two ahead.
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        rn = issue(slot);
+        if (r.blk == r.nb - 1 && (r.tk & 31))
+            fold_block<HD, KIND, true>(f, qh, ql, r.blk * 32, r.tk, grp, a.score_l2, m_run, l_run, o);
+        else
+            fold_block<HD, KIND, false>(f, qh, ql, r.blk * 32, r.tk, grp, a.score_l2, m_run, l_run, o);
+        // The end of a segment: a head's last block, or the range's.
+        if (r.blk == r.nb - 1 || pp == p_end - 1) {
+            const float lsum = sum4grp(l_run);
+            // A whole head: its block 0 lies in this range too.
+            if (r.blk == r.nb - 1 && pp - r.blk >= p_first) {
+                if (col < group) {
+                    float* out = a.out + a.out_off + (size_t)r.s * a.out_stride + (size_t)r.h * n + (size_t)col * HD;
+                    const float inv = 1.0f / lsum;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        *reinterpret_cast<floatx4*>(out + 16 * t + 4 * grp) = o[t] * inv;
+                }
+                vm_ops += NT;
+            } else {
+                // Part of a head: O [g][HD] and (m, l) [g] into this wave's
+                // slot, with agent-scope (coherent) stores.
+                const int sl = pp == p_end - 1 ? 1 : 0;
+                const size_t slot_i = (size_t)u * 2 + sl;
+                float* po = a.part + slot_i * (16 * HD);
+                float* pml = a.part + a.ml_off + slot_i * 32;
+                const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(po, 0, 16 * HD * 4, 0x00020000);
+                typedef float v4 __attribute__((ext_vector_type(4)));
+                if (col < group) {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        __builtin_amdgcn_raw_buffer_store_b128(v4{o[t][0], o[t][1], o[t][2], o[t][3]}, rp,
+                                                               (col * HD + 16 * t + 4 * grp) * 4, 0, 16);  // sc1
+                    if (grp == 0) {
+                        typedef float v2 __attribute__((ext_vector_type(2)));
+                        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(pml, 0, 128, 0x00020000);
+                        __builtin_amdgcn_raw_buffer_store_b64(v2{m_run, lsum}, rm, 8 * col, 0, 16);  // sc1
+                    }
+                }
+                vm_ops += NT + 1;
+                const long hs = rdlane64(sq.base, r.s) + (long)r.h * r.nb;
+                if (sl) pend1 = hs;
+                else pend0 = hs;
+            }
+        }
+    };
+
+    for (long p = p_first; p < p_end; p += 2) {
+        fold_at(0, p, r0, r0);
+        if (p + 1 >= p_end) break;
+        fold_at(1, p + 1, r1, r1);
+    }
+
+    // Arrivals: after every partial store has completed, count this wave at
+    // each head it published to; the last arriver merges that head.
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int sl = 0; sl < 2; ++sl) {
+        const long hs = sl ? pend1 : pend0;
+        if (hs < 0) continue;
+        const SkPos r = sk_locate(sq, hs, kv);
+        const long he = hs + r.nb;
+        const int hd_i = r.s * kv + r.h;
+        const long c0 = sk_owner(hs, nw, total), c1 = sk_owner(he - 1, nw, total);
+        unsigned prev = 0;
+        if (lane == 0) prev = __hip_atomic_fetch_add(a.ctr + (size_t)hd_i * CTR_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __shfl(prev, 0, 64);
+        if (prev != (unsigned)(c1 - c0)) continue;
+        // Merge, in range order, the partials of contributors c0 .. c1: lane
+        // owns float4 e4 = lane + 64 j of the head's [g][HD] context (two j
+        // per pass), and folds contributors in with an online rescale, MB
+        // contributors' loads in flight at a time.
+        // Every contributor but the last publishes the head as the segment
+        // ending its range (slot 1); the last one, as slot 1 only if its
+        // range ends with the head.
+        const int last_sl = sk_first(c1 + 1, nw, total) == he ? 1 : 0;
+        auto slot_of = [&](long c) { return (size_t)c * 2 + (c < c1 ? 1 : last_sl); };
+        float* out = a.out + a.out_off + (size_t)(hd_i / kv) * a.out_stride + (size_t)(hd_i % kv) * n;
+        constexpr int MB = 12;
+        for (int j0 = 0; j0 * 64 < n / 4; j0 += 2) {
+            int e4[2], g[2];
+            bool on[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                e4[j] = lane + 64 * (j0 + j);
+                on[j] = e4[j] < n / 4;
+                g[j] = on[j] ? (4 * e4[j]) / HD : 0;
+            }
+            float M[2] = {ninf(), ninf()}, L[2] = {0.0f, 0.0f};
+            floatx4 acc[2] = {zero_f4(), zero_f4()};
+            for (long cb = c0; cb <= c1; cb += MB) {
+                float4 ov[MB][2];
+                float2 mv[MB][2];
+#pragma unroll
+                for (int k = 0; k < MB; ++k) {
+                    const bool live = cb + k <= c1;
+                    const size_t si = live ? slot_of(cb + k) : 0;
+                    const Region ro = region(a.part + si * (16 * HD), live ? 16 * HD * 4 : 0);
+                    const Region rm = region(a.part + a.ml_off + si * 32, live ? 32 * 4 : 0);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        ov[k][j] = ld_region4<true>(ro, (uint32_t)(on[j] ? e4[j] * 16 : 0));
+                        mv[k][j] = ld_region2<true>(rm, (uint32_t)(g[j] * 8));
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < MB; ++k) {
+                    if (cb + k > c1) continue;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const float mn = fmaxf(M[j], mv[k][j].x);
+                        const float al = ex2(M[j] - mn), be = ex2(mv[k][j].x - mn);
+                        M[j] = mn;
+                        L[j] = L[j] * al + mv[k][j].y * be;
+                        acc[j] = acc[j] * al + floatx4{ov[k][j].x, ov[k][j].y, ov[k][j].z, ov[k][j].w} * be;
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (on[j]) *reinterpret_cast<floatx4*>(out + 4 * e4[j]) = acc[j] * (1.0f / L[j]);
+        }
+        if (lane == 0) __hip_atomic_store(a.ctr + (size_t)hd_i * CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 #define DECODE_INST(HD, KIND, VA) template __global__ void attn_decode_kernel<HD, KIND, VA>(DecodeArgs);
 DECODE_INST(64, KV_F16, 16) DECODE_INST(128, KV_F16, 16) DECODE_INST(64, KV_F16, 8) DECODE_INST(128, KV_F16, 8)
 DECODE_INST(64, KV_F32, 16) DECODE_INST(128, KV_F32, 16) DECODE_INST(64, KV_F32, 8) DECODE_INST(128, KV_F32, 8)
 DECODE_INST(64, KV_T16, 16) DECODE_INST(128, KV_T16, 16) DECODE_INST(64, KV_TQ8, 16) DECODE_INST(128, KV_TQ8, 16)
 
+template __global__ void attn_decode_sk_kernel<64>(DecodeArgs);
+template __global__ void attn_decode_sk_kernel<128>(DecodeArgs);
 template __global__ void attn_merge_kernel<64>(DecodeArgs);
 template __global__ void attn_merge_kernel<128>(DecodeArgs);
 
@@ -880,7 +1295,17 @@ static hipError_t launch_merge(int hd, const DecodeArgs& a, int kv_heads, int ns
 }
 
 static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
-    dim3 grid = a.dyn ? dim3(a.items) : dim3(a.splits, kv_heads, nseq);
+    if (a.sk) {
+        dim3 grid(a.items), block(DT);
+        if (kind != KV_TQ8) return hipErrorInvalidValue;
+        const size_t qdyn = (size_t)DW * 2 * a.group * hd * sizeof(float);  // raw query buffers (<= 64 KB)
+        if (hd == 128) hipLaunchKernelGGL((attn_decode_sk_kernel<128>), grid, block, qdyn, st, a);
+        else if (hd == 64) hipLaunchKernelGGL((attn_decode_sk_kernel<64>), grid, block, qdyn, st, a);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+        return hipErrorInvalidValue;
+    }
+    dim3 grid(a.splits, kv_heads, nseq);
     dim3 block(DT);
     const int esz = kind == KV_F32 ? 4 : 2;
     const int va = (kind == KV_T16 || kind == KV_TQ8) ? 16 : (((long)a.cap * esz) % 16 == 0 ? 16 : 8);
@@ -898,7 +1323,7 @@ static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_head
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
     hipError_t e = launch_attn(hd, kind, a, kv_heads, nseq, st);
-    if (e != hipSuccess || !a.two_phase || a.splits <= 1) return e;
+    if (e != hipSuccess || a.sk || !a.two_phase || a.splits <= 1) return e;
     return launch_merge(hd, a, kv_heads, nseq, st);
 }
 

@@ -59,6 +59,6 @@ __host__ __device__ inline int tq8_v_off(int kk, int d) {
     const int t = d >> 4, c = d & 15, g = kk >> 3, j = kk & 7;
     return ((t >> 1) * 64 + (c + 16 * g)) * 16 + 8 * (t & 1) + j;
 }
-__host__ __device__ inline long tq8_block_bytes(int hd) { return 2L * 32 * hd + 2L * 32 * (hd / 32) * 2; }
+__host__ __device__ constexpr long tq8_block_bytes(int hd) { return 2L * 32 * hd + 2L * 32 * (hd / 32) * 2; }
 
 }  // namespace llmtie
