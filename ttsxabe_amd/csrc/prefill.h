@@ -28,6 +28,13 @@ struct PrefillArgs {
     int scale_q;      // the scale goes on q before rounding (else on the scores)
     size_t v_bytes;   // PF_F16: bytes of the V cache allocation (bounds the tile loads)
     int out_f16;      // fast path: write the context as f16 (else f32)
+    // Fast path, set by launch_prefill: the launch is a 1-D grid whose
+    // workgroup L runs item (L % 8) * (items / 8) + L / 8 of the
+    // (head group, position block) list, group-major, so the eight XCDs
+    // (workgroups are dealt to them round-robin) each take a contiguous run
+    // of whole groups and read their K/V through their own L2 (C3 at 8192
+    // rows: 767 -> 679 us).
+    int xcd, nrb;
 };
 
 // f32 K/V (a cache or the column blocks of stacked rows) -> the tiled f16

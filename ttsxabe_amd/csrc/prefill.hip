@@ -415,9 +415,16 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     const int gb = a.gb;
     const int pb = QPW * (PW / gb);
     const int group = a.heads / a.kv_heads;
-    const int bx = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    const int h = blockIdx.y * gb + wave % gb;
-    const int kh = (blockIdx.y * gb) / group;
+    int rb = blockIdx.x, gy = blockIdx.y;
+    if (a.xcd) {
+        const int item = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+        gy = item / a.nrb;
+        rb = item % a.nrb;
+    }
+    // Causal: heaviest position blocks first.
+    const int bx = a.causal ? a.nrb - 1 - rb : rb;
+    const int h = gy * gb + wave % gb;
+    const int kh = (gy * gb) / group;
     const int bp0 = bx * pb;
     const int p0 = bp0 + (wave / gb) * QPW;
     const int ktot = a.past + a.tq;
@@ -760,9 +767,14 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
     const bool fast = (kind == PF_T16 || (kind == PF_F16 && a.v_bytes <= 0xffffffffull)) &&
                       (a.scale_q || a.scale > 0.0f) && !getenv("LLMTIE_PREFILL_STAGED");
     if (fast) {
+        PrefillArgs b = a;
+        b.nrb = (int)grid.x;
+        const unsigned items = grid.x * grid.y;
+        b.xcd = items % 8 == 0 && !(getenv("LLMTIE_PREFILL_XCD") && !atoi(getenv("LLMTIE_PREFILL_XCD")));
+        const dim3 g = b.xcd ? dim3(items) : grid;
 #define F(HD, KIND, NQ)                                                                    \
     if (hd == HD && kind == KIND && nqt == NQ) {                                           \
-        hipLaunchKernelGGL((flash_fwd_kernel<HD, KIND, NQ>), grid, block, 0, st, a);       \
+        hipLaunchKernelGGL((flash_fwd_kernel<HD, KIND, NQ>), g, block, 0, st, b);          \
         return hipGetLastError();                                                          \
     }
         F(64, PF_F16, 1) F(64, PF_F16, 2) F(128, PF_F16, 1) F(128, PF_F16, 2)
