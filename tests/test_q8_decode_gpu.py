@@ -148,3 +148,10 @@ def test_ragged_mix_and_head_width_64(gpu):
 def test_more_than_64_sequences_take_the_planned_grid(gpu):
     tk = (oracle.uniform_int(70, 33, 1, 300)).astype(np.int32)
     check_batch(gpu, 128, 8, 2, 70, 320, tk, np.arange(70, dtype=np.int32), 43)
+
+
+@pytest.mark.parametrize("hd,heads,kv", [(128, 16, 1), (64, 8, 8), (128, 64, 4)])
+def test_group_widths(gpu, hd, heads, kv):
+    """GQA groups of 16 (the largest query buffers) and 1 (MHA)."""
+    tk = (oracle.uniform_int(9, 34 + heads, 1, 700)).astype(np.int32)
+    check_batch(gpu, hd, heads, kv, 9, 704, tk, np.arange(9, dtype=np.int32)[::-1].copy(), 44 + heads)
