@@ -673,78 +673,69 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     }
 }
 
-// One workgroup per (head, 32-key block): the block's K rows and V rows (or
-// V^T rows) are read with coalesced 16-byte loads into LDS, then written out
-// as the tiled layout's 16-byte chunks -- K chunk (T, s, lane) holds key
-// 8*(col/4) + 4T + col%4, dims 32s + 8grp .. +7; V chunk (t, lane) holds dim
-// 16t + col, keys 8grp .. +7 (kvlayout.h). f32 -> f16 rounds to nearest
-// even, as the kernels' own staging does. VKEY: V is stored keys-contiguous
-// (V^T rows, the f32 cache); otherwise dims-contiguous (stacked rows).
+// f32 K/V -> the tiled f16 layout, one thread per 16-byte output chunk (the
+// layout is [head][block][fragment][lane], so consecutive threads write
+// consecutive chunks). K chunk (T, s, lane) holds key 8*(col/4) + 4T + col%4,
+// dims 32s + 8grp .. +7: 32 contiguous bytes of one K row. V chunk (t, lane)
+// holds dim 16t + col, keys 8grp .. +7: 32 contiguous bytes of one V^T row
+// (VKEY, the f32 cache), or one float from each of 8 V rows (stacked rows,
+// consecutive lanes reading consecutive dims). Keys past nkeys are zeros;
+// f32 -> f16 rounds to nearest even, as the kernels' own staging does.
 template <int HD, bool VKEY>
 __global__ __launch_bounds__(256) void f32_to_t16_kernel(const float* __restrict__ k, long khs, long kps,
                                                          const float* __restrict__ v, long vhs, long vps, long vds,
-                                                         half_t* __restrict__ dst, int nkeys, int nblk) {
-    constexpr int NS = HD / 32, NT = HD / 16;
-    __shared__ float ks[32][HD + 1];
-    __shared__ float vs[VKEY ? HD : 32][VKEY ? 33 : HD + 1];
-    const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int live = min(32, nkeys - 32 * b);  // keys of this block that exist
-    // K rows: 32 x HD floats, float4 per thread-step.
-    for (int i = tid; i < 32 * HD / 4; i += 256) {
-        const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
-        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (r < live) x = *reinterpret_cast<const float4*>(k + h * khs + (long)(32 * b + r) * kps + c);
-        ks[r][c] = x.x; ks[r][c + 1] = x.y; ks[r][c + 2] = x.z; ks[r][c + 3] = x.w;
-    }
-    if constexpr (VKEY) {
-        // V^T rows: HD x 32 keys, keys contiguous.
-        for (int i = tid; i < HD * 8; i += 256) {
-            const int d = i / 8, c = 4 * (i % 8);
-            const float* src = v + h * vhs + (long)d * vds + 32 * b + c;
-            float x[4];
+                                                         half_t* __restrict__ dst, int nkeys, int nblk, long nchunk) {
+    constexpr int NS = HD / 32, NT = HD / 16, CPB = (2 * NS + NT) * 64;  // chunks per block
+    const long c = (long)blockIdx.x * 256 + threadIdx.x;
+    if (c >= nchunk) return;
+    const long hb = c / CPB;
+    const int w = (int)(c % CPB), f = w / 64, lane = w % 64, col = lane & 15, grp = lane >> 4;
+    const int h = (int)(hb / nblk), b = (int)(hb % nblk);
+    float x[8];
+    if (f < 2 * NS) {
+        const int T = f / NS, s = f % NS;
+        const int key = 32 * b + 8 * (col >> 2) + 4 * T + (col & 3);
+        if (key < nkeys) {
+            const float4* p = reinterpret_cast<const float4*>(k + h * khs + (long)key * kps + 32 * s + 8 * grp);
+            const float4 a0 = p[0], a1 = p[1];
+            x[0] = a0.x; x[1] = a0.y; x[2] = a0.z; x[3] = a0.w; x[4] = a1.x; x[5] = a1.y; x[6] = a1.z; x[7] = a1.w;
+        } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) x[j] = c + j < live ? src[j] : 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) vs[d][c + j] = x[j];
+            for (int j = 0; j < 8; ++j) x[j] = 0.0f;
         }
     } else {
-        for (int i = tid; i < 32 * HD / 4; i += 256) {
-            const int r = i / (HD / 4), c = 4 * (i % (HD / 4));
-            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (r < live) x = *reinterpret_cast<const float4*>(v + h * vhs + (long)(32 * b + r) * vps + c);
-            vs[r][c] = x.x; vs[r][c + 1] = x.y; vs[r][c + 2] = x.z; vs[r][c + 3] = x.w;
+        const int d = 16 * (f - 2 * NS) + col, k0 = 32 * b + 8 * grp;
+        if constexpr (VKEY) {
+            const float* p = v + h * vhs + (long)d * vds + k0;
+            if (k0 + 8 <= nkeys) {
+                const float4 a0 = reinterpret_cast<const float4*>(p)[0], a1 = reinterpret_cast<const float4*>(p)[1];
+                x[0] = a0.x; x[1] = a0.y; x[2] = a0.z; x[3] = a0.w; x[4] = a1.x; x[5] = a1.y; x[6] = a1.z; x[7] = a1.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = k0 + j < nkeys ? p[j] : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = k0 + j < nkeys ? v[h * vhs + (long)(k0 + j) * vps + d] : 0.0f;
         }
     }
-    __syncthreads();
-    half8* out = reinterpret_cast<half8*>(dst) + ((size_t)h * nblk + b) * (2 * NS + NT) * 64;
-    for (int c = tid; c < 2 * NS * 64; c += 256) {
-        const int ln = c % 64, col = ln & 15, grp = ln >> 4, f = c / 64, T = f / NS, s = f % NS;
-        const int key = 8 * (col >> 2) + 4 * T + (col & 3);
-        half8 x;
+    half8 y;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = to_h(ks[key][32 * s + 8 * grp + j]);
-        out[c] = x;
-    }
-    for (int c = tid; c < NT * 64; c += 256) {
-        const int ln = c % 64, col = ln & 15, grp = ln >> 4, t = c / 64;
-        const int d = 16 * t + col;
-        half8 x;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = to_h(VKEY ? vs[d][8 * grp + j] : vs[8 * grp + j][d]);
-        out[2 * NS * 64 + c] = x;
-    }
+    for (int j = 0; j < 8; ++j) y[j] = to_h(x[j]);
+    reinterpret_cast<half8*>(dst)[c] = y;
 }
 
 hipError_t launch_f32_to_t16(const float* k, long khs, long kps, const float* v, long vhs, long vps, long vds,
                              uint16_t* dst, int kv, int hd, int nkeys, hipStream_t st) {
     const int nblk = tiled_nblk(nkeys);
-    const dim3 grid(nblk, kv);
+    const long nchunk = (long)kv * nblk * (hd / 8) * 64;  // chunks per block: 2 * hd/32 (K) + hd/16 (V)
+    const dim3 grid((unsigned)((nchunk + 255) / 256));
     half_t* d = reinterpret_cast<half_t*>(dst);
     const bool vkey = vps == 1;
 #define CV(HD, VK)                                                                                      \
     if (hd == HD && vkey == VK) {                                                                       \
         hipLaunchKernelGGL((f32_to_t16_kernel<HD, VK>), grid, dim3(256), 0, st, k, khs, kps, v, vhs, vps, vds, d, \
-                           nkeys, nblk);                                                                \
+                           nkeys, nblk, nchunk);                                                        \
         return hipGetLastError();                                                                       \
     }
     CV(64, false) CV(64, true) CV(128, false) CV(128, true)
