@@ -248,11 +248,13 @@ int compute_units() {
 // wave taking whole 32-key blocks, and never more than the merge can hold.
 void plan_decode(size_t tk_max, size_t units, size_t group, int& nit, int& splits) {
     const size_t max_splits = std::min<size_t>(DECODE_MAX_SPLITS, DECODE_MAX_SPLIT_ROWS / std::max<size_t>(1, group));
-    // Measured on MI355X: a lone sequence decodes fastest over ~128
-    // workgroups (the split merge's cost grows with the count faster than the
-    // stream gains); a batch wants about three splits per (sequence, kv head)
-    // at its longest context so the long sequences do not set the time alone.
-    size_t target = std::max<size_t>(128, 3 * units);
+    // Measured on MI355X: a lone sequence decodes fastest over ~256
+    // workgroups (C2: 10.99 us at 128, 10.69 at 256, flat beyond; with the
+    // arrival counters on separate lines the in-launch merge no longer grows
+    // costlier with the split count); a batch wants about three splits per
+    // (sequence, kv head) at its longest context so the long sequences do not
+    // set the time alone.
+    size_t target = std::max<size_t>(256, 3 * units);
     if (const char* e = getenv("LLMTIE_DECODE_WGS")) target = std::max(1, atoi(e));
     const size_t blocks = (tk_max + 31) / 32;
     size_t want = std::max<size_t>(1, target / std::max<size_t>(1, units));
@@ -277,9 +279,11 @@ void plan_decode(size_t tk_max, size_t units, size_t group, int& nit, int& split
 // the last-arriving workgroup of each head.
 int two_phase_merge(int splits, size_t units) {
     if (const char* e = getenv("LLMTIE_DECODE_TWO_PHASE")) return atoi(e) ? 1 : 0;
-    // Past ~192 workgroups the in-launch hand-off (coherent stores, a wait,
-    // an atomic per workgroup) costs more than a second launch does.
-    return (size_t)splits * units >= 192 ? 1 : 0;
+    // The in-launch hand-off (coherent stores, a wait, an atomic per
+    // workgroup, each counter on its own line) measured faster than a second
+    // launch up to 512 workgroups (C2 at 256: 10.69 vs 12.12 us); a second
+    // launch merges beyond 1024.
+    return (size_t)splits * units > 1024 ? 1 : 0;
 }
 
 int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hipStream_t st) {
