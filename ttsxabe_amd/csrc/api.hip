@@ -286,6 +286,24 @@ int two_phase_merge(int splits, size_t units) {
     return (size_t)splits * units > 1024 ? 1 : 0;
 }
 
+// Floats of the (m, l) area per (sequence, kv head): whole 256-byte lines,
+// so no line is shared by two heads' partials.
+size_t ml_stride(int splits, size_t group) { return ((size_t)splits * group * 2 + 63) / 64 * 64; }
+
+// Whether a host-planned in-launch merge keeps every head on one XCD: each
+// XCD's run of (launch / 8) items (the dispatcher deals workgroups to the
+// eight XCDs of gfx950 round-robin) holds whole heads. A partitioned device
+// with 4, 2 or 1 XCDs still groups them: workgroups L = x mod 8 then share
+// XCD x mod (its XCD count).
+int xcd_local(int splits, size_t units, int two_phase) {
+    if (const char* e = getenv("LLMTIE_DECODE_XCD")) {
+        if (!atoi(e)) return 0;
+    }
+    const size_t total = (size_t)splits * units;
+    if (two_phase || splits <= 1 || total % 8 != 0) return 0;
+    return (total / 8) % (size_t)splits == 0 ? 1 : 0;
+}
+
 int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hipStream_t st) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -361,7 +379,8 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     const size_t group = heads / kv_heads;
     int nit, splits;
     plan_decode(tk, kv_heads, group, nit, splits);
-    const size_t part = kv_heads * (size_t)splits * group * (hd + 2);
+    const size_t mls = ml_stride(splits, group);
+    const size_t part = kv_heads * ((size_t)splits * group * hd + mls);
     const long ml_off = (long)(kv_heads * (size_t)splits * group * hd);
     int r = ensure_scratch(scratch, part, kv_heads * CTR_STRIDE, S(stream));
     if (r != LLMTIE_OK) return r;
@@ -388,7 +407,9 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     a.qscale = scale_q ? scale : 1.0f;
     a.nit = nit;
     a.splits = splits;
+    a.ml_stride = (long)mls;
     a.two_phase = two_phase_merge(splits, kv_heads);
+    a.xcd = xcd_local(splits, kv_heads, a.two_phase);
     return launched("attn_decode", launch_decode((int)hd, kind, a, (int)kv_heads, 1, S(stream)));
 }
 
@@ -504,7 +525,8 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     // batch through the host-planned grid (splits of the longest sequence).
     const bool sk = nseq <= 64 && !getenv("LLMTIE_DECODE_STATIC");
     const int items = sk ? compute_units() : 0;
-    size_t part = nseq * kv_heads * (size_t)splits * group * (head_dim + 2);
+    const size_t mls = ml_stride(splits, group);
+    size_t part = nseq * kv_heads * ((size_t)splits * group * head_dim + mls);
     long ml_off = (long)(nseq * kv_heads * (size_t)splits * group * head_dim);
     if (sk) {
         const size_t slots2 = (size_t)items * 4 * 2;
@@ -534,7 +556,9 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     a.qscale = scale_q ? scale : 1.0f;
     a.nit = nit;
     a.splits = splits;
+    a.ml_stride = (long)mls;
     a.two_phase = sk ? 0 : two_phase_merge(splits, kv_heads * nseq);
+    a.xcd = sk ? 0 : xcd_local(splits, kv_heads * nseq, a.two_phase);
     a.sk = sk ? 1 : 0;
     a.nseq = (int)nseq;
     a.items = items;

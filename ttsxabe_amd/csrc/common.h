@@ -121,9 +121,13 @@ __device__ __forceinline__ float ld_coherent(const float* p) {
 
 // Wide reads of a workgroup-uniform region through a buffer resource: one
 // 8- or 16-byte load per lane, reads past `bytes` return zeros (so a ragged
-// tail needs no branch), and COH selects the agent-scope cache policy (sc1,
-// the policy of an agent-scope relaxed atomic load) for data another
-// workgroup of this launch published with st_coherent.
+// tail needs no branch), and AUX is the cache policy: AUX_AGENT (sc1, the
+// policy of an agent-scope relaxed atomic load) for data another workgroup
+// of this launch published with st_coherent, AUX_XCD (sc0) for data another
+// workgroup on the same XCD stored into the shared L2 in this launch, 0 for
+// data an earlier launch wrote.
+constexpr int AUX_AGENT = 16;
+constexpr int AUX_XCD = 1;
 struct Region {
     __amdgpu_buffer_rsrc_t r;
 };
@@ -131,15 +135,15 @@ __device__ __forceinline__ Region region(const void* base, uint32_t bytes) {
     // Word 3 = 0x00020000: raw (untyped) buffer access on gfx9-family parts.
     return Region{__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000)};
 }
-template <bool COH>
+template <int AUX>
 __device__ __forceinline__ float4 ld_region4(const Region& g, uint32_t off) {
     typedef float v4 __attribute__((ext_vector_type(4)));
-    const v4 x = __builtin_amdgcn_raw_buffer_load_b128(g.r, off, 0, COH ? 16 : 0);
+    const v4 x = __builtin_amdgcn_raw_buffer_load_b128(g.r, off, 0, AUX);
     return make_float4(x[0], x[1], x[2], x[3]);
 }
-template <bool COH>
+template <int AUX>
 __device__ __forceinline__ float2 ld_region2(const Region& g, uint32_t off) {
     typedef float v2 __attribute__((ext_vector_type(2)));
-    const v2 x = __builtin_amdgcn_raw_buffer_load_b64(g.r, off, 0, COH ? 16 : 0);
+    const v2 x = __builtin_amdgcn_raw_buffer_load_b64(g.r, off, 0, AUX);
     return make_float2(x[0], x[1]);
 }

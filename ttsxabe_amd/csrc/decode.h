@@ -25,6 +25,7 @@ struct DecodeArgs {
     float* twin_scales;      // its per-32 scales
     float* part;             // split partials: O area, then the (m, l) area at ml_off
     long ml_off;             // floats from part to the (m, l) area
+    long ml_stride;          // floats of the (m, l) area per (sequence, kv head): whole 256-byte lines
     unsigned* ctr;           // arrival counters, one per (sequence, kv head) every CTR_STRIDE words, zero between calls
     const int* tk_arr;       // per-sequence live lengths (batched) or null
     const int* slot_arr;     // per-sequence cache slot (batched) or null
@@ -45,6 +46,13 @@ struct DecodeArgs {
     // (sequence, kv head, 32-key block) list. Partial slots: two per wave, O
     // [16][hd] floats each, then the (m, l) area at ml_off, 32 floats each.
     int sk, nseq, items;
+    // XCD-local split hand-off (xcd != 0; host-planned grid, in-launch
+    // merge): a 1-D grid whose workgroup L runs item (L % 8) * (grid / 8) +
+    // L / 8 (sequence-major, then kv head, then split). Workgroups are dealt
+    // to the XCDs round-robin and the host sets xcd only when every XCD's run
+    // of items holds whole heads, so a head's splits, partials and merge all
+    // stay in one XCD's L2: plain partial stores, L2 reads in the merge.
+    int xcd;
 };
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);

@@ -418,12 +418,13 @@ __device__ __forceinline__ void emit(float* out, int8_t* tc, float* ts, size_t i
 // of DT threads, with every load issued before any is waited on (one memory
 // round trip): first the (m, l) pairs the weights need, then the partial
 // columns, so the weights are computed while the columns are in flight.
-// COH: the partials were handed over with coherent stores inside this launch
-// (read them with the same agent-scope policy); otherwise a launch boundary
-// separates writer and reader. `lds` holds >= 4096 floats.
+// AUX: the cache policy of the partial loads (ld_region4): AUX_AGENT for
+// partials handed over with coherent stores inside this launch, AUX_XCD for
+// partials stored into this XCD's L2 inside this launch, 0 when a launch
+// boundary separates writer and reader. `lds` holds >= 4096 floats.
 // Thread t owns float4 column c = t % C of the [g][HD] partial (C = n / 4)
 // and the splits s = t / C, t / C + R, ... (R = DT / C phases).
-template <int HD, bool COH>
+template <int HD, int AUX>
 __device__ __forceinline__ void merge_head(const float* po, const float* pml, int nsplit, int group, float* lds,
                                            float* gl, float* out, int8_t* tc, float* ts, size_t obase) {
     const int tid = threadIdx.x;
@@ -443,7 +444,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
 #pragma unroll
     for (int k = 0; k < MK; ++k) {
         ml[k] = make_float2(0.f, 0.f);
-        if (64 * k < nsplit && g0 < group) ml[k] = ld_region2<COH>(rml, (uint32_t)(((lane + 64 * k) * group + g0) * 8));
+        if (64 * k < nsplit && g0 < group) ml[k] = ld_region2<AUX>(rml, (uint32_t)(((lane + 64 * k) * group + g0) * 8));
     }
     // This thread's partial columns, up to U splits in flight.
     constexpr int U = 16;
@@ -454,7 +455,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
     for (int u = 0; u < U; ++u) {
         const int sp = phase + u * R;
         x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (has && u * R < nsplit) x[u] = ld_region4<COH>(ro, (uint32_t)(((size_t)sp * n + 4 * c4) * 4));
+        if (has && u * R < nsplit) x[u] = ld_region4<AUX>(ro, (uint32_t)(((size_t)sp * n + 4 * c4) * 4));
     }
     // Weights: for query head g (a wave per g), M_g = max_s m, w_sg = 2^(m - M),
     // L_g = sum_s l w, reduced across the wave's lanes.
@@ -462,7 +463,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
         if (g != g0) {
 #pragma unroll
             for (int k = 0; k < MK; ++k)
-                if (64 * k < nsplit) ml[k] = ld_region2<COH>(rml, (uint32_t)(((lane + 64 * k) * group + g) * 8));
+                if (64 * k < nsplit) ml[k] = ld_region2<AUX>(rml, (uint32_t)(((lane + 64 * k) * group + g) * 8));
         }
         float mx = ninf();
 #pragma unroll
@@ -500,7 +501,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
         // Splits beyond the first U * R (long contexts): more rounds.
         for (int s0 = phase + U * R; s0 < nsplit; s0 += U * R) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) x[u] = ld_region4<COH>(ro, (uint32_t)(((size_t)(s0 + u * R) * n + 4 * c4) * 4));
+            for (int u = 0; u < U; ++u) x[u] = ld_region4<AUX>(ro, (uint32_t)(((size_t)(s0 + u * R) * n + 4 * c4) * 4));
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int sp = s0 + u * R;
@@ -518,7 +519,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
         const int g = (4 * w) / HD;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int sp = 0; sp < nsplit; ++sp) {
-            const float4 y = ld_region4<COH>(ro, (uint32_t)(((size_t)sp * n + 4 * w) * 4));
+            const float4 y = ld_region4<AUX>(ro, (uint32_t)(((size_t)sp * n + 4 * w) * 4));
             const float wt = wts[sp * group + g];
             acc.x += y.x * wt;
             acc.y += y.y * wt;
@@ -549,7 +550,14 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
-    const int split = blockIdx.x, h = blockIdx.y, seq = blockIdx.z, nit = a.nit;
+    int split = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
+    const int nit = a.nit;
+    if (a.xcd) {
+        const int item = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+        split = item % a.splits;
+        h = (item / a.splits) % a.kv_heads;
+        seq = item / (a.splits * a.kv_heads);
+    }
     const int group = a.group;
     const int tk = a.tk_arr ? min(a.tk_arr[seq], a.tk) : a.tk;
     const int slot = a.slot_arr ? a.slot_arr[seq] : 0;
@@ -712,7 +720,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     // the O area, (m, l) per g in the ML area, 16 bytes a store.
     const size_t head = (size_t)seq * a.kv_heads + h;
     float* po = a.part + (head * a.splits) * n;
-    float* pml = a.part + a.ml_off + (head * a.splits) * group * 2;
+    float* pml = a.part + a.ml_off + head * a.ml_stride;
     auto partial4 = [&](int e4) {
         const int g = (4 * e4) / HD, d = (4 * e4) % HD;
         float f[DW];
@@ -742,11 +750,15 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         return;
     }
     // Cross-workgroup hand-off without cache-wide fences: the partial is
-    // stored with agent-scope (coherent) stores, the stores are waited for,
-    // and only then is the arrival counted; the last arriver reads the
-    // partials with agent-scope loads. A release/acquire fence pair would
-    // write back and invalidate the whole L2 of the XCD on every workgroup,
-    // which measured several times the cost of the attention itself.
+    // stored, the stores are waited for, and only then is the arrival
+    // counted; the last arriver reads the partials. Across XCDs the stores
+    // and the merger's loads are agent-scope (coherent past the XCDs'
+    // separate L2s); with a head's splits all on one XCD (a.xcd) plain
+    // stores into the shared L2 and L2 reads suffice. A release/acquire
+    // fence pair would write back and invalidate the whole L2 of the XCD on
+    // every workgroup, which measured several times the cost of the
+    // attention itself.
+    const bool loc = a.xcd != 0;
     {
         const __amdgpu_buffer_rsrc_t rp =
             __builtin_amdgcn_make_buffer_rsrc(po + (size_t)split * n, 0, n * 4, 0x00020000);
@@ -754,13 +766,20 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         for (int e4 = tid; e4 < n / 4; e4 += DT) {
             const floatx4 x = partial4(e4);
             const v4 y = {x[0], x[1], x[2], x[3]};
-            __builtin_amdgcn_raw_buffer_store_b128(y, rp, e4 * 16, 0, 16);  // sc1: agent scope
+            if (loc) __builtin_amdgcn_raw_buffer_store_b128(y, rp, e4 * 16, 0, 0);
+            else __builtin_amdgcn_raw_buffer_store_b128(y, rp, e4 * 16, 0, AUX_AGENT);
         }
     }
     if (tid < group) {
         const floatx4 x = ml(tid);
-        st_coherent(pml + ((size_t)split * group + tid) * 2, x[0]);
-        st_coherent(pml + ((size_t)split * group + tid) * 2 + 1, x[1]);
+        float* d = pml + ((size_t)split * group + tid) * 2;
+        if (loc) {
+            d[0] = x[0];
+            d[1] = x[1];
+        } else {
+            st_coherent(d, x[0]);
+            st_coherent(d + 1, x[1]);
+        }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -772,7 +791,8 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     __syncthreads();
     if (!last) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    merge_head<HD, true>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
+    if (loc) merge_head<HD, AUX_XCD>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
+    else merge_head<HD, AUX_AGENT>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -794,7 +814,7 @@ __global__ __launch_bounds__(DT) void attn_merge_kernel(DecodeArgs a) {
     const int n = group * HD;
     const size_t head = (size_t)seq * a.kv_heads + h;
     const float* po = a.part + (head * a.splits) * n;
-    const float* pml = a.part + a.ml_off + (head * a.splits) * group * 2;
+    const float* pml = a.part + a.ml_off + head * a.ml_stride;
     float* out = a.out + a.out_off + (size_t)seq * a.out_stride;
     int8_t* tc = nullptr;
     float* ts = nullptr;
@@ -803,7 +823,7 @@ __global__ __launch_bounds__(DT) void attn_merge_kernel(DecodeArgs a) {
         tc = a.twin_codes + oo;
         ts = a.twin_scales + (oo >> 5);
     }
-    merge_head<HD, false>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
+    merge_head<HD, 0>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
 }
 
 // ------------------------------------------------------------------------
@@ -1252,8 +1272,8 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
                     const Region rm = region(a.part + a.ml_off + si * 32, live ? 32 * 4 : 0);
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        ov[k][j] = ld_region4<true>(ro, (uint32_t)(on[j] ? e4[j] * 16 : 0));
-                        mv[k][j] = ld_region2<true>(rm, (uint32_t)(g[j] * 8));
+                        ov[k][j] = ld_region4<AUX_AGENT>(ro, (uint32_t)(on[j] ? e4[j] * 16 : 0));
+                        mv[k][j] = ld_region2<AUX_AGENT>(rm, (uint32_t)(g[j] * 8));
                     }
                 }
 #pragma unroll
@@ -1305,7 +1325,7 @@ static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_head
         return hipGetLastError();
         return hipErrorInvalidValue;
     }
-    dim3 grid(a.splits, kv_heads, nseq);
+    const dim3 grid = a.xcd ? dim3(a.splits * kv_heads * nseq) : dim3(a.splits, kv_heads, nseq);
     dim3 block(DT);
     const int esz = kind == KV_F32 ? 4 : 2;
     const int va = (kind == KV_T16 || kind == KV_TQ8) ? 16 : (((long)a.cap * esz) % 16 == 0 ? 16 : 8);
