@@ -855,6 +855,11 @@ __device__ __forceinline__ long rdlane64(long v, int l) {
     const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((unsigned long)v >> 32), l);
     return (long)(((unsigned long)hi << 32) | lo);
 }
+__device__ __forceinline__ long rdfirst64(long v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)((unsigned long)v >> 32));
+    return (long)(((unsigned long)hi << 32) | lo);
+}
 
 // Waves of the launch that take part (never more than there are blocks, so
 // every wave's range is non-empty), and wave u's range [first(u), first(u+1)).
@@ -1226,74 +1231,193 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     }
 
     // Arrivals: after every partial store has completed, count this wave at
-    // each head it published to; the last arriver merges that head.
+    // each head it published part of (at most two), both atomics in one round
+    // trip; the last arriver at a head merges it.
     __builtin_amdgcn_s_waitcnt(0);
-    for (int sl = 0; sl < 2; ++sl) {
-        const long hs = sl ? pend1 : pend0;
-        if (hs < 0) continue;
+    pend0 = rdfirst64(pend0);
+    pend1 = rdfirst64(pend1);
+    struct Head {
+        long c0, c1;  // its contributors, in range order
+        int last_sl;  // the last contributor's slot for it
+        int idx;      // sequence * kv + kv head
+    };
+    auto head_at = [&](long hs) {
         const SkPos r = sk_locate(sq, hs, kv);
         const long he = hs + r.nb;
-        const int hd_i = r.s * kv + r.h;
-        const long c0 = sk_owner(hs, nw, total), c1 = sk_owner(he - 1, nw, total);
-        unsigned prev = 0;
-        if (lane == 0) prev = __hip_atomic_fetch_add(a.ctr + (size_t)hd_i * CTR_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        prev = __shfl(prev, 0, 64);
-        if (prev != (unsigned)(c1 - c0)) continue;
-        // Merge, in range order, the partials of contributors c0 .. c1: lane
-        // owns float4 e4 = lane + 64 j of the head's [g][HD] context (two j
-        // per pass), and folds contributors in with an online rescale, MB
-        // contributors' loads in flight at a time.
+        Head h;
+        h.c0 = sk_owner(hs, nw, total);
+        h.c1 = sk_owner(he - 1, nw, total);
         // Every contributor but the last publishes the head as the segment
         // ending its range (slot 1); the last one, as slot 1 only if its
         // range ends with the head.
-        const int last_sl = sk_first(c1 + 1, nw, total) == he ? 1 : 0;
-        auto slot_of = [&](long c) { return (size_t)c * 2 + (c < c1 ? 1 : last_sl); };
-        float* out = a.out + a.out_off + (size_t)(hd_i / kv) * a.out_stride + (size_t)(hd_i % kv) * n;
-        constexpr int MB = 12;
-        for (int j0 = 0; j0 * 64 < n / 4; j0 += 2) {
-            int e4[2], g[2];
-            bool on[2];
+        h.last_sl = sk_first(h.c1 + 1, nw, total) == he ? 1 : 0;
+        h.idx = r.s * kv + r.h;
+        h.c0 = rdfirst64(h.c0);
+        h.c1 = rdfirst64(h.c1);
+        h.last_sl = __builtin_amdgcn_readfirstlane(h.last_sl);
+        h.idx = __builtin_amdgcn_readfirstlane(h.idx);
+        return h;
+    };
+    Head h0 = head_at(pend0 >= 0 ? pend0 : 0), h1 = head_at(pend1 >= 0 ? pend1 : 0);
+    unsigned prev0 = 0, prev1 = 0;
+    if (lane == 0) {
+        if (pend0 >= 0)
+            prev0 = __hip_atomic_fetch_add(a.ctr + (size_t)h0.idx * CTR_STRIDE, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        if (pend1 >= 0)
+            prev1 = __hip_atomic_fetch_add(a.ctr + (size_t)h1.idx * CTR_STRIDE, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Lane 0's counts (the whole wave is active), kept in scalar registers
+    // so the merge's addressing stays wave-uniform.
+    prev0 = __builtin_amdgcn_readfirstlane(prev0);
+    prev1 = __builtin_amdgcn_readfirstlane(prev1);
+    const bool m0 = pend0 >= 0 && prev0 == (unsigned)(h0.c1 - h0.c0);
+    const bool m1 = pend1 >= 0 && prev1 == (unsigned)(h1.c1 - h1.c0);
+    if (!m0 && !m1) return;
+    // The heads to merge: A, then B when there are two.
+    const int nm = (int)m0 + (int)m1;
+    const Head A = m0 ? h0 : h1, B = h1;
+    const long cntA = A.c1 - A.c0 + 1, cntB = nm > 1 ? B.c1 - B.c0 + 1 : 0;
+    auto slot_of = [&](const Head& h, long c) -> size_t {
+        return (size_t)c * 2 + (c < h.c1 ? 1 : h.last_sl);
+    };
+    // Each head's contributors are merged, in range order, in chunks of KC
+    // counted from the head's first: a chunk's (m, l) pairs go straight into
+    // LDS (half of the wave's idle ring per head, lane-strided dword loads),
+    // its max M is taken once, and every contributor then adds 2^(m - M)
+    // times its l and O. The arithmetic of a head depends only on its own
+    // contributors, never on which wave merges it or what it merges beside.
+    // O moves in batches of MB contributors (both heads' chunks as one
+    // list), two float4 loads each: with the (m, l) loads at most ~60
+    // vector-memory instructions, under the 63 a wave can have outstanding.
+    // Lane owns float4 e4 = lane + 64 j of a head's [g][HD] context.
+    constexpr int MB = 24;
+    constexpr int HALF_F = ((2 * BB / 4 - 64) / 2) / 64 * 64;  // floats of LDS per head
+    const int gp = 2 * group;                            // (m, l) floats per contributor
+    const int KC = HALF_F / gp;
+    float* const mls = reinterpret_cast<float*>(&ring[wave][0][0]);
+    float* const Ms = mls + 2 * HALF_F;  // [head][16]: the chunk's running max per query head
+    const float* const mlp = a.part + a.ml_off;
+    for (int j0 = 0; j0 * 64 < n / 4; j0 += 2) {
+        int e4[2], g[2];
+        bool on[2];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                e4[j] = lane + 64 * (j0 + j);
-                on[j] = e4[j] < n / 4;
-                g[j] = on[j] ? (4 * e4[j]) / HD : 0;
+        for (int j = 0; j < 2; ++j) {
+            e4[j] = lane + 64 * (j0 + j);
+            on[j] = e4[j] < n / 4;
+            g[j] = on[j] ? (4 * e4[j]) / HD : 0;
+        }
+        float M[2][2] = {{ninf(), ninf()}, {ninf(), ninf()}}, L[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+        floatx4 acc[2][2] = {{zero_f4(), zero_f4()}, {zero_f4(), zero_f4()}};
+        for (long t0 = 0; t0 < cntA || t0 < cntB; t0 += KC) {
+            const int nA = (int)max(0L, min((long)KC, cntA - t0)), nB = (int)max(0L, min((long)KC, cntB - t0));
+            const int nc = nA + nB;
+            // The previous chunk's LDS reads are done before it is overwritten.
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const Head& h = hh ? B : A;
+                const int nh = hh ? nB : nA;
+                for (int i = 0; i * 64 < nh * gp; ++i) {
+                    const int fi = 64 * i + lane, k = fi / gp;
+                    // Lanes past the chunk read a harmless float (slot 0's).
+                    const float* src = mlp + (k < nh ? slot_of(h, h.c0 + t0 + k) * 32 + fi % gp : 0);
+                    __builtin_amdgcn_global_load_lds(src, mls + hh * HALF_F + 64 * i, 4, 0, AUX_AGENT);
+                }
             }
-            float M[2] = {ninf(), ninf()}, L[2] = {0.0f, 0.0f};
-            floatx4 acc[2] = {zero_f4(), zero_f4()};
-            for (long cb = c0; cb <= c1; cb += MB) {
+            for (int cb = 0; cb < nc; cb += MB) {
                 float4 ov[MB][2];
+#pragma unroll
+                for (int k = 0; k < MB; ++k) {
+                    const int e = cb + k;
+                    const bool live = e < nc, inB = e >= nA;
+                    // Wave-uniform: kept scalar so the load needs no waterfall.
+                    const size_t si = (unsigned)__builtin_amdgcn_readfirstlane(
+                        (int)(!live ? 0 : inB ? slot_of(B, B.c0 + t0 + (e - nA)) : slot_of(A, A.c0 + t0 + e)));
+                    const Region ro = region(a.part + si * (16 * HD), live ? 16 * HD * 4 : 0);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        ov[k][j] = ld_region4<AUX_AGENT>(ro, (uint32_t)(on[j] ? e4[j] * 16 : 0));
+                }
+                wait_vm<0>();
+                if (cb == 0) {
+                    // The chunk's max per head and column (reads clamped to
+                    // the chunk: repeats do not move a max), then the running
+                    // sums rescaled to it.
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int nh = hh ? nB : nA;
+                        if (nh == 0) continue;
+                        const float* ml = mls + hh * HALF_F;
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            float bm = ninf();
+                            for (int c = 0; c < nh; c += 8) {
+                                float x[8];
+#pragma unroll
+                                for (int q = 0; q < 8; ++q) x[q] = ml[min(c + q, nh - 1) * gp + 2 * g[j]];
+#pragma unroll
+                                for (int q = 0; q < 8; ++q) bm = fmaxf(bm, x[q]);
+                            }
+                            const float mn = fmaxf(M[hh][j], bm);
+                            const float al = ex2(M[hh][j] - mn);
+                            M[hh][j] = mn;
+                            L[hh][j] *= al;
+                            acc[hh][j] = acc[hh][j] * al;
+                            if (on[j] && (4 * e4[j]) % HD == 0) Ms[hh * 16 + g[j]] = mn;
+                        }
+                    }
+                    // The chunk's (m, l) pairs become (w, l w), w = 2^(m - M),
+                    // in place, one pair per lane: one exponential per pair
+                    // rather than per lane and contributor.
+                    for (int i = lane; i < nc * group; i += 64) {
+                        const int k = i / group, gg = i % group, hh = k >= nA ? 1 : 0;
+                        float2* pr = reinterpret_cast<float2*>((hh ? mls + HALF_F + (k - nA) * gp : mls + k * gp) + 2 * gg);
+                        const float2 v = *pr;
+                        const float w = ex2(v.x - Ms[hh * 16 + gg]);
+                        *pr = make_float2(w, v.y * w);
+                    }
+                }
                 float2 mv[MB][2];
 #pragma unroll
                 for (int k = 0; k < MB; ++k) {
-                    const bool live = cb + k <= c1;
-                    const size_t si = live ? slot_of(cb + k) : 0;
-                    const Region ro = region(a.part + si * (16 * HD), live ? 16 * HD * 4 : 0);
-                    const Region rm = region(a.part + a.ml_off + si * 32, live ? 32 * 4 : 0);
+                    const int e = min(cb + k, nc - 1);
+                    const float* ml = e >= nA ? mls + HALF_F + (e - nA) * gp : mls + e * gp;
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        ov[k][j] = ld_region4<AUX_AGENT>(ro, (uint32_t)(on[j] ? e4[j] * 16 : 0));
-                        mv[k][j] = ld_region2<AUX_AGENT>(rm, (uint32_t)(g[j] * 8));
-                    }
+                    for (int j = 0; j < 2; ++j) mv[k][j] = *reinterpret_cast<const float2*>(ml + 2 * g[j]);
                 }
 #pragma unroll
                 for (int k = 0; k < MB; ++k) {
-                    if (cb + k > c1) continue;
+                    const int e = cb + k;
+                    if (e >= nc) continue;
+                    const int hb = e >= nA ? 1 : 0;
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const float mn = fmaxf(M[j], mv[k][j].x);
-                        const float al = ex2(M[j] - mn), be = ex2(mv[k][j].x - mn);
-                        M[j] = mn;
-                        L[j] = L[j] * al + mv[k][j].y * be;
-                        acc[j] = acc[j] * al + floatx4{ov[k][j].x, ov[k][j].y, ov[k][j].z, ov[k][j].w} * be;
+                    for (int hh = 0; hh < 2; ++hh) {
+                        if (hh != hb) continue;
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            L[hh][j] += mv[k][j].y;
+                            acc[hh][j] += floatx4{ov[k][j].x, ov[k][j].y, ov[k][j].z, ov[k][j].w} * mv[k][j].x;
+                        }
                     }
                 }
             }
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            if (hh >= nm) continue;
+            const int hi = hh ? B.idx : A.idx;
+            float* out = a.out + a.out_off + (size_t)(hi / kv) * a.out_stride + (size_t)(hi % kv) * n;
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                if (on[j]) *reinterpret_cast<floatx4*>(out + 4 * e4[j]) = acc[j] * (1.0f / L[j]);
+                if (on[j]) *reinterpret_cast<floatx4*>(out + 4 * e4[j]) = acc[hh][j] * (1.0f / L[hh][j]);
         }
-        if (lane == 0) __hip_atomic_store(a.ctr + (size_t)hd_i * CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0) {
+        __hip_atomic_store(a.ctr + (size_t)A.idx * CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (nm > 1)
+            __hip_atomic_store(a.ctr + (size_t)B.idx * CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
