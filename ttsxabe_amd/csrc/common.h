@@ -110,6 +110,30 @@ __device__ __forceinline__ float sum4grp(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Whole-wave max and sum, every lane getting the same bits, on the VALU:
+// DPP xor-1 and xor-2 within quads, the half-row and row mirrors (lane i
+// with 7 - i, then 15 - i), then the two permlane swaps across rows and
+// halves. Each step combines a lane with a partner that combines it back,
+// so partners compute identical values (no LDS-crossbar round trips).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4e>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+    return max4grp(v);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = v + dpp_f<0xb1>(v);
+    v = v + dpp_f<0x4e>(v);
+    v = v + dpp_f<0x141>(v);
+    v = v + dpp_f<0x140>(v);
+    return sum4grp(v);
+}
+
 // Agent-scope (device-coherent) 32-bit store and loads: visible across the
 // XCDs' separate L2s without a cache-wide fence.
 __device__ __forceinline__ void st_coherent(float* p, float v) {

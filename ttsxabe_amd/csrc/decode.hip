@@ -437,15 +437,18 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
     const Region ro = region(po, (uint32_t)((size_t)nsplit * n * 4));
     const Region rml = region(pml, (uint32_t)((size_t)nsplit * group * 8));
 
-    // (m, l) of query head g0 = wave for splits lane + 64k.
+    // (m, l) of query head g0 = wave for splits lane + 64k. Every load here
+    // is unconditional (past the regions' ends the buffer bounds check
+    // returns zeros), so the compiler can count them and the weights wait
+    // only for the (m, l) loads, not for the partial columns behind them.
     constexpr int MK = DECODE_MAX_SPLITS / 64;
+    constexpr uint32_t OUT = 0x80000000u;  // an offset past any region (all are < 2 GB)
     float2 ml[MK];
     const int g0 = wave;
 #pragma unroll
-    for (int k = 0; k < MK; ++k) {
-        ml[k] = make_float2(0.f, 0.f);
-        if (64 * k < nsplit && g0 < group) ml[k] = ld_region2<AUX>(rml, (uint32_t)(((lane + 64 * k) * group + g0) * 8));
-    }
+    for (int k = 0; k < MK; ++k)
+        ml[k] = ld_region2<AUX>(rml, 64 * k < nsplit && g0 < group ? (uint32_t)(((lane + 64 * k) * group + g0) * 8) : OUT);
+    __builtin_amdgcn_sched_barrier(0);  // the (m, l) loads go out first
     // This thread's partial columns, up to U splits in flight.
     constexpr int U = 16;
     const int c4 = tid % C, phase = tid / C;
@@ -454,8 +457,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int sp = phase + u * R;
-        x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (has && u * R < nsplit) x[u] = ld_region4<AUX>(ro, (uint32_t)(((size_t)sp * n + 4 * c4) * 4));
+        x[u] = ld_region4<AUX>(ro, has && sp < nsplit ? (uint32_t)(((size_t)sp * n + 4 * c4) * 4) : OUT);
     }
     // Weights: for query head g (a wave per g), M_g = max_s m, w_sg = 2^(m - M),
     // L_g = sum_s l w, reduced across the wave's lanes.
@@ -469,8 +471,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
 #pragma unroll
         for (int k = 0; k < MK; ++k)
             if (lane + 64 * k < nsplit) mx = fmaxf(mx, ml[k].x);
-#pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+        mx = wave_max(mx);
         float L = 0.0f;
 #pragma unroll
         for (int k = 0; k < MK; ++k) {
@@ -481,8 +482,7 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
                 L += ml[k].y * w;
             }
         }
-#pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) L += __shfl_xor(L, o2, 64);
+        L = wave_sum(L);
         if (lane == 0) gl[g] = L;
     }
     __syncthreads();
