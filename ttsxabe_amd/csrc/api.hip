@@ -335,7 +335,9 @@ int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hi
         s->ctr_cap = 0;
         e = hipMalloc(&s->ctr, want * sizeof(unsigned));
         if (e != hipSuccess) return driver("allocating", e);
-        e = hipMemsetAsync(s->ctr, 0, want * sizeof(unsigned), st);
+        // Zeroed by a kernel on the caller's stream (a memset node inside a
+        // captured graph is not to be relied on).
+        e = launch_fill_u32(s->ctr, want, 0u, st);
         if (e != hipSuccess) return driver("zeroing", e);
         s->ctr_cap = want;
     }

@@ -57,4 +57,7 @@ struct DecodeArgs {
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);
 
+// Fills n words with v (a kernel, so it may sit inside a captured graph).
+hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t st);
+
 }  // namespace llmtie

@@ -1465,6 +1465,17 @@ static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_head
     return hipErrorInvalidValue;
 }
 
+__global__ void fill_u32_kernel(unsigned* p, size_t n, unsigned v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks), dim3(256), 0, st, p, n, v);
+    return hipGetLastError();
+}
+
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
     hipError_t e = launch_attn(hd, kind, a, kv_heads, nseq, st);
     if (e != hipSuccess || a.sk || !a.two_phase || a.splits <= 1) return e;
