@@ -121,8 +121,9 @@ class CpuStack:
             q = linear(x, w[f"{l}.wq"])
             k = linear(x, w[f"{l}.wk"])
             v = linear(x, w[f"{l}.wv"])
-            q = _rope(q, n, c.heads, hd, c.theta, past).reshape(n, -1)
-            k = _rope(k, n, c.kv_heads, hd, c.theta, past).reshape(n, -1)
+            fd = w.get("rope_freqs")  # Llama-3 per-frequency divisors (rope.rs:83-126), if bound
+            q = _rope(q, n, c.heads, hd, c.theta, past, fd).reshape(n, -1)
+            k = _rope(k, n, c.kv_heads, hd, c.theta, past, fd).reshape(n, -1)
             kk = through_f16(k).reshape(n, c.kv_heads, hd).transpose(1, 0, 2)
             vv = through_f16(v).reshape(n, c.kv_heads, hd).transpose(1, 0, 2)
             self.k[l] = np.concatenate([self.k[l], kk], axis=1)

@@ -52,3 +52,33 @@ def test_random_llama_stack_decodes_like_the_cpu(gpu, layout):
         ids = [top_c]
     assert dev.past == cpu.past == 261 and dev.cap == 512
     assert ties <= 2, f"{layout}: {ties} of 12 steps were numerical ties (random weights should rarely tie)"
+
+
+@pytest.mark.parametrize("layout", ["reference", "tiled"])
+def test_a_gguf_llama_decodes_like_the_cpu(gpu, layout, tmp_path):
+    """The same check on weights read back from a llama.cpp-style GGUF (F16
+    and Q8_0 matrices, q/k rows permuted for interleaved RoPE, a Llama-3
+    rope_freqs table): the binding must undo the permutation and carry the
+    frequency divisors to this library's RoPE for the argmax to hold."""
+    from ttsxabe_amd.llama_gguf import load_llama_gguf
+    from ttsxabe_amd.stack import LlamaStack
+    from tests.test_gguf import llama_gguf
+    cfg = StackConfig()
+    w = random_weights(cfg, SEED + 7)
+    held = llama_gguf(tmp_path / "m.gguf", cfg, w, rope_freqs=np.linspace(1.0, 8.0, cfg.head_dim // 2,
+                                                                           dtype=np.float32))
+    c, wl = load_llama_gguf(tmp_path / "m.gguf")
+    cpu = CpuStack(c, held)
+    dev = LlamaStack(gpu, c, wl, layout)
+    rng = np.random.default_rng(SEED + 8)
+    ids = [int(t) for t in rng.integers(0, c.vocab, 40)]
+    for step in range(6):
+        lc = cpu.forward(ids)
+        lg = dev.forward(ids).float().cpu().numpy()
+        scale = float(np.abs(lc).max())
+        err = float(np.abs(lc - lg).max())
+        assert err < 5e-3 * scale, f"{layout} step {step}: logit error {err:.3g} of scale {scale:.3g}"
+        srt = np.sort(lc)
+        if float(srt[-1] - srt[-2]) > 2 * err + 1e-6:
+            assert int(lg.argmax()) == int(lc.argmax()), f"{layout} step {step}"
+        ids = [int(lc.argmax())]

@@ -73,6 +73,7 @@ class LlamaStack:
         n, past, hd = len(ids), self.past, c.head_dim
         self._grow(past + n)
         scale = float(np.float32(hd) ** np.float32(-0.5))
+        fd = w.get("rope_freqs")  # Llama-3 per-frequency RoPE divisors, when the checkpoint has them
         h = w["embed"][torch.as_tensor(list(ids), device=g.device)]
         for l in range(c.layers):
             x = self._norm(h, w[f"{l}.attn_norm"])
@@ -82,24 +83,24 @@ class LlamaStack:
             if self.layout == "tiled":
                 t = self.tc[l]
                 if n == 1:
-                    g.t16_rope_cache(q, 0, k, 0, v, 0, None, c.heads, c.theta, past, t)
+                    g.t16_rope_cache(q, 0, k, 0, v, 0, fd, c.heads, c.theta, past, t)
                     ctx = g.attn_decode_t16(q, t, c.heads, past + 1, scale, False, self.scratch)
                 else:
-                    g.rope(q, 0, n, c.heads, hd, c.theta, past)
-                    g.rope(k, 0, n, c.kv_heads, hd, c.theta, past)
+                    g.rope_scaled(q, 0, fd, n, c.heads, hd, c.theta, past)
+                    g.rope_scaled(k, 0, fd, n, c.kv_heads, hd, c.theta, past)
                     g.t16_append(k, 0, t, n, past, False)
                     g.t16_append(v, 0, t, n, past, True)
                     ctx = g.flash_attn_t16(q, t, n, past, c.heads, scale, True)
             else:
                 kc, vc = self.kc[l], self.vc[l]
                 if n == 1:
-                    g.rope_cache_f16(q, 0, k, 0, v, 0, None, c.heads, c.kv_heads, hd, c.theta, past, kc, vc,
+                    g.rope_cache_f16(q, 0, k, 0, v, 0, fd, c.heads, c.kv_heads, hd, c.theta, past, kc, vc,
                                      self.cap)
                     ctx = g.attn_decode_f16(q, kc, vc, c.heads, c.kv_heads, hd, past + 1, self.cap, scale, False,
                                             self.scratch)
                 else:
-                    g.rope(q, 0, n, c.heads, hd, c.theta, past)
-                    g.rope(k, 0, n, c.kv_heads, hd, c.theta, past)
+                    g.rope_scaled(q, 0, fd, n, c.heads, hd, c.theta, past)
+                    g.rope_scaled(k, 0, fd, n, c.kv_heads, hd, c.theta, past)
                     g.cache_append_f16(k, 0, kc, n, c.kv_heads, hd, self.cap, past, False)
                     g.cache_append_f16(v, 0, vc, n, c.kv_heads, hd, self.cap, past, True)
                     ctx = g.flash_attn_f16(q, kc, vc, n, past, c.heads, c.kv_heads, hd, self.cap, scale, True)
