@@ -686,11 +686,17 @@ __global__ __launch_bounds__(256) void f32_to_t16_kernel(const float* __restrict
                                                          const float* __restrict__ v, long vhs, long vps, long vds,
                                                          half_t* __restrict__ dst, int nkeys, int nblk, long nchunk) {
     constexpr int NS = HD / 32, NT = HD / 16, CPB = (2 * NS + NT) * 64;  // chunks per block
-    const long c = (long)blockIdx.x * 256 + threadIdx.x;
-    if (c >= nchunk) return;
-    const long hb = c / CPB;
-    const int w = (int)(c % CPB), f = w / 64, lane = w % 64, col = lane & 15, grp = lane >> 4;
-    const int h = (int)(hb / nblk), b = (int)(hb % nblk);
+    // Work item i runs (block, head) = (i / kv, i % kv): workgroups running
+    // together read the same source rows (every head's columns of one
+    // 32-key block) rather than one head's columns of rows spread over the
+    // whole tensor. The chunk written is at its layout place, [head][block].
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nchunk) return;
+    const long kvh = nchunk / ((long)nblk * CPB);
+    const long bh = i / CPB;
+    const int w = (int)(i % CPB), f = w / 64, lane = w % 64, col = lane & 15, grp = lane >> 4;
+    const int h = (int)(bh % kvh), b = (int)(bh / kvh);
+    const long c = ((long)h * nblk + b) * CPB + w;
     float x[8];
     if (f < 2 * NS) {
         const int T = f / NS, s = f % NS;
