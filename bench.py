@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", metavar="NAME",
                     help="run one secondary workload (c3_prefill_8192_steady, c3_prefill_512, c4_encoder, "
-                         "c5_q8_batch_decode) and print its line alone, for profiling runs")
+                         "c5_q8_batch_decode, practical_peaks) and print its line alone, for profiling runs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB a few times (the known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -236,10 +236,12 @@ def bench_q8_batch(torch, g, steps, warmup):
 def practical_peaks(torch):
     """What this box sustains outside the hot path, measured in the same run
     as context for the spec peaks the fractions use: an 8192^3 f16 GEMM
-    through torch.matmul (the vendor GEMM library) and a 1 GiB device copy
-    (bytes read + written). Under sustained dense MFMA work the part runs
-    power-limited below its 2.4 GHz peak clock, so the GEMM figure is the
-    practical MFMA ceiling."""
+    through torch.matmul (the vendor GEMM library), a 1 GiB device copy
+    (bytes read + written), and this repository's two probes
+    (ttsxabe_amd/csrc/peaks.hip): back-to-back 16x16x32 f16 MFMAs from
+    registers on every SIMD (the MFMA rate at the clock the part holds under
+    dense work; it runs power-limited below its 2.4 GHz peak clock) and a
+    streaming read of 1 GiB (the HBM read rate a kernel can reach)."""
     def timed(fn, reps):
         for _ in range(3):
             fn()
@@ -259,8 +261,23 @@ def practical_peaks(torch):
     src = torch.ones(2 ** 29, dtype=torch.float16, device="cuda")
     dst = torch.empty_like(src)
     t_copy = timed(lambda: dst.copy_(src), 20)
+    del dst
+    import ctypes
+    from ttsxabe_amd.build import PEAKS_LIB
+    pk = ctypes.CDLL(str(PEAKS_LIB))
+    pk.llmtie_peak_mfma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    pk.llmtie_peak_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(max(cus, 1) * 8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    iters = 20000
+    t_mfma = timed(lambda: pk.llmtie_peak_mfma(st, sink.data_ptr(), cus, iters), 5)
+    nbytes = src.numel() * 2
+    t_read = timed(lambda: pk.llmtie_peak_read(st, src.data_ptr(), nbytes, sink.data_ptr(), cus * 8), 10)
     return {"f16_gemm_8192_tflops": round(2 * n ** 3 / t_gemm / 1e12, 1),
-            "copy_1gib_gbs": round(2 * src.numel() * 2 / t_copy / 1e9, 1)}
+            "copy_1gib_gbs": round(2 * src.numel() * 2 / t_copy / 1e9, 1),
+            "mfma_f16_loop_tflops": round(cus * 8 * iters * 8 * 16384 / t_mfma / 1e12, 1),
+            "hbm_read_1gib_gbs": round(nbytes / t_read / 1e9, 1)}
 
 
 def cpu_baseline(seconds: float):
@@ -351,6 +368,7 @@ def main():
             "c3_prefill_512": lambda: bench_prefill(torch, g, 512, 32, 8, 128, a.steps, a.warmup, a.layers),
             "c4_encoder": lambda: bench_encoder(torch, g, 1500, 20, 64, a.steps, a.warmup, a.layers),
             "c5_q8_batch_decode": lambda: bench_q8_batch(torch, g, a.steps, a.warmup),
+            "practical_peaks": lambda: practical_peaks(torch),
         }
         if a.only not in only:
             print(json.dumps({"error": f"--only takes one of {sorted(only)}"}))

@@ -16,6 +16,10 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libllmtie_hip.so"
+# The bench's measurement probes (peak MFMA rate, HBM read rate): a separate
+# library so the attention ABI stays the reference's operators only.
+PEAKS_LIB = PKG / "libllmtie_peaks.so"
+PEAKS_SRC = "peaks.hip"
 SOURCES = ["api.hip", "decode.hip", "prefill.hip", "kvcache.hip"]
 ARCH = "gfx950"
 # Packed-FP32 instructions stay off (they have given silent wrong results on
@@ -70,6 +74,9 @@ def build(verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc(), *FLAGS, *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB)
+    ptmp = PEAKS_LIB.with_suffix(".so.tmp")
+    _run([hipcc(), *FLAGS, str(CSRC / PEAKS_SRC), "-o", str(ptmp)], verbose)
+    os.replace(ptmp, PEAKS_LIB)
     return LIB
 
 
