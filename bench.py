@@ -198,13 +198,16 @@ def bench_encoder(torch, g, t, heads, hd, steps, warmup, layers):
 
 def bench_q8_batch(torch, g, steps, warmup):
     """C5: 32 sequences, one launch over a tiled Q8_0 cache; lengths from the
-    seeded U[256, 8192] draw; two layers' caches alternate (> 2x the LLC)."""
+    seeded U[256, 8192] draw. Eight layers' caches (4.6 GB, far beyond the
+    LLC) are decoded in turn, one launch each, per graph replay, as a model's
+    layers are: with fewer launches per replay the replay's own gap would be
+    spread over too few of them."""
     from ttsxabe_amd.gpu import DecodeScratch, KvCacheQ8
     from tests import configs
     nseq, heads, kv, hd, cap = 32, 32, 8, 128, 8192
     tk = configs.c5_lengths(nseq=nseq)
     bytes_layer = 2 * kv * (hd + 2 * hd // 32) * int(tk.sum())  # 272 * 8 * sum(tk)
-    L = max(2, math.ceil(2 * LLC_BYTES / bytes_layer))
+    L = max(8, math.ceil(2 * LLC_BYTES / bytes_layer))
     gen = torch.Generator(device="cuda").manual_seed(5)
     caches = []
     nb = hd // 32
