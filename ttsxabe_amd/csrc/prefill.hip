@@ -36,11 +36,11 @@
 #include "kvlayout.h"
 
 // LDS fragment reads kept in flight ahead of the MFMAs that use them in the
-// tile loop's software pipeline (measured on MI355X: 6 and 8 both beat 4 -
-// C3@512 14.5 -> 14.0 us, C3@8192 631 -> 623 us - at two waves per SIMD the
-// LDS latency is otherwise not covered).
+// tile loop's software pipeline, at most the pipeline's reads (measured on
+// MI355X: 4 -> 6 -> 10 took C3@512 14.5 -> 14.0 -> 13.8 us and C3@8192
+// 631 -> 613 -> 611 us; 12 and 16 were slower again).
 #ifndef LLMTIE_PF_PD
-#define LLMTIE_PF_PD 6
+#define LLMTIE_PF_PD 10
 #endif
 
 namespace llmtie {
@@ -544,7 +544,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
             }
         // Software pipeline: PD fragment reads ahead of the MFMAs using them.
         {
-            constexpr int NR = 4 * NS, PD = LLMTIE_PF_PD;
+            constexpr int NR = 4 * NS, PD = LLMTIE_PF_PD < NR ? LLMTIE_PF_PD : NR;
             __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
 #pragma unroll
             for (int i2 = 0; i2 < NR - PD; ++i2) {
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
                 for (int u = 0; u < NQT; ++u) o[t][u] = mfma16(af, pb[hf][u], o[t][u]);
             }
         {
-            constexpr int NR = 2 * NT, PD = LLMTIE_PF_PD;
+            constexpr int NR = 2 * NT, PD = LLMTIE_PF_PD < NR ? LLMTIE_PF_PD : NR;
             __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
 #pragma unroll
             for (int i2 = 0; i2 < NR - PD; ++i2) {
