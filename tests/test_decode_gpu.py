@@ -36,6 +36,10 @@ CASES = [
     (40, 40, 128, 1500, 1536, True, False),
     (20, 20, 64, 1500, 1500, True, True),
     (8, 8, 64, 5000, 5056, False, True),
+    # GQA groups of 3 (not in kernels.rs): the split merge's phase count is 5
+    # at head_dim 64, not a power of two.
+    (12, 4, 64, 3000, 3008, True, False),
+    (6, 2, 128, 5000, 5056, True, False),
 ]
 
 

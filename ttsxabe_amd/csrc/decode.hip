@@ -37,6 +37,7 @@
 // the last workgroup of the head (agent-scope counter) merges all splits in
 // split order and resets the counter to zero. The result does not depend on
 // which workgroup finishes last, so repeated calls are bit-identical.
+#include <type_traits>
 #include "common.h"
 #include "decode.h"
 #include "kvlayout.h"
@@ -529,10 +530,28 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
         reinterpret_cast<float4*>(red)[w] = acc;
     }
     __syncthreads();
-    for (int e = tid; e < n; e += DT) {
-        float acc = 0.0f;
-        for (int r = 0; r < R; ++r) acc += red[r * n + e];
-        emit(out, tc, ts, obase + e, acc / gl[e / HD]);
+    // Sum the phases. R (1 to 16) is fixed by the head's shape; with a
+    // compile-time bound every LDS read of an element is issued before the
+    // first is waited on (a runtime-bounded sum waited on each read in turn).
+    // Reads are clamped to the R rows written and the sum masked to them.
+    auto finish = [&](auto rr) {
+        constexpr int RR = decltype(rr)::value;
+        for (int e = tid; e < n; e += DT) {
+            float v[RR];
+#pragma unroll
+            for (int r = 0; r < RR; ++r) v[r] = red[min(r, R - 1) * n + e];
+            float acc = 0.0f;
+#pragma unroll
+            for (int r = 0; r < RR; ++r) acc += r < R ? v[r] : 0.0f;
+            emit(out, tc, ts, obase + e, acc / gl[e / HD]);
+        }
+    };
+    switch (R) {
+        case 1: finish(std::integral_constant<int, 1>{}); break;
+        case 2: finish(std::integral_constant<int, 2>{}); break;
+        case 4: finish(std::integral_constant<int, 4>{}); break;
+        case 8: finish(std::integral_constant<int, 8>{}); break;
+        default: finish(std::integral_constant<int, 16>{}); break;  // any other R <= 16
     }
 }
 
