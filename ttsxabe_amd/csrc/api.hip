@@ -462,8 +462,12 @@ int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint1
     a.os = (int)d;
     a.scale_q = 1;
     a.out_f16 = 1;
-    return prefill_via_t16("flash_attn_rows", S(stream), a, 64, pick_nqt(t, heads, 1), qkv + d, 64, (long)(3 * d),
-                           qkv + 2 * d, 64, (long)(3 * d), 1, PF_ROWS);
+    // The staged kernel reads the stacked f32 rows directly. The faster
+    // route through a tiled f16 copy (prefill_via_t16 with the stacked-rows
+    // conversion) is switched off: one MI355X run of it at 1500 rows x 20
+    // heads ended in a GPU memory fault, identical code and inputs had passed
+    // before, and no cause has been found in its indexing or ordering.
+    return launched("flash_attn_rows", launch_prefill(64, PF_ROWS, pick_nqt(t, heads, 1), a, S(stream)));
 }
 
 int llmtie_attn_decode_f16(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
