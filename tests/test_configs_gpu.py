@@ -27,6 +27,24 @@ def check(want, got, rows, heads, hd, what):
     assert cos.min() >= MIN_COS, f"{what}: head cosine {cos.min()}"
 
 
+def test_c1_f32_causal_mha_prefill(gpu):
+    """Config 1 (f32 causal MHA, 8/8/64, 128 tokens, no RoPE) through the HIP
+    f32-cache prefill, against the reference's CPU f32 chain at the north
+    star's bar, and against the reference's f64 prefill rule
+    (kernels.rs:2290-2374)."""
+    c = configs.c1_cpu()
+    t, heads, hd = c["t"], c["heads"], c["hd"]
+    cpu = oracle.prefill_f32(c["q"], c["k"], c["v"], t, heads, heads, hd, c["scale"], True)
+    kc = np.ascontiguousarray(c["k"].reshape(t, heads, hd).transpose(1, 0, 2)).ravel()  # [kv][cap][hd]
+    vc = np.ascontiguousarray(c["v"].reshape(t, heads, hd).transpose(1, 2, 0)).ravel()  # [kv][hd][cap]
+    got = down(gpu.flash_attn(up(c["q"]), up(kc), up(vc), t, 0, heads, heads, hd, t, c["scale"], True))
+    check(cpu, got, t, heads, hd, "C1 f32 prefill vs the CPU f32 chain")
+    want, spread = oracle.prefill_ref(c["q"], heads * hd, kc, vc, t, 0, heads, heads, hd, t, c["scale"], True)
+    tol = 2e-4 + 1e-2 * np.abs(want) + 1e-2 * spread
+    err = np.abs(want - got.astype(np.float64))
+    assert (err <= tol).all() and float((err / tol).max()) < 0.5
+
+
 def test_c2_llama3_gqa_decode(gpu):
     from ttsxabe_amd.gpu import DecodeScratch
     c = configs.c2_decode()

@@ -219,3 +219,96 @@ def test_tiled_f16_producers_are_the_reference_producers_repacked(gpu, hd):
     # Positions past `live` inside the last copied block are carried along
     # whole (they were zero in the source), so the images agree everywhere.
     assert np.array_equal(got, want)
+
+
+def _ref_scatter(fill, vals, kv, hd, cap, past, transposed):
+    """Rows [n][kv][hd] written at positions past.. of K [kv][cap][hd]
+    (transposed: V^T [kv][hd][cap]) over `fill`, in numpy."""
+    out = fill.copy()
+    n = vals.shape[0]
+    if transposed:
+        out.reshape(kv, hd, cap)[:, :, past:past + n] = vals.transpose(1, 2, 0)
+    else:
+        out.reshape(kv, cap, hd)[:, past:past + n, :] = vals.transpose(1, 0, 2)
+    return out
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_append_writes_the_reference_layout_bit_for_bit(gpu, f16, transposed):
+    """cache_append / cache_append_f16 against a numpy scatter of the rows
+    (rounded by the oracle's RNE f16 for the f16 cache) into the reference
+    layouts, every other position untouched (kernels.rs:1919-2069, 3013,
+    2849)."""
+    n, kv, hd, cap, past, off = 7, 3, 64, 40, 9, 5
+    src = oracle.seq(off + n * kv * hd, 301)
+    fill = oracle.seq(kv * cap * hd, 302)
+    rows = src[off:].reshape(n, kv, hd)
+    if f16:
+        want = _ref_scatter(oracle.f32_to_f16(fill), oracle.f32_to_f16(rows.ravel()).reshape(n, kv, hd), kv, hd, cap,
+                            past, transposed)
+        dst = up_f16(fill)
+        gpu.cache_append_f16(up(src), off, dst, n, kv, hd, cap, past, transposed)
+        assert np.array_equal(down(dst).view(np.uint16), want)
+    else:
+        want = _ref_scatter(fill, rows, kv, hd, cap, past, transposed)
+        dst = up(fill)
+        gpu.cache_append(up(src), off, dst, n, kv, hd, cap, past, transposed)
+        assert np.array_equal(down(dst).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_growth_restrides_the_reference_layout_bit_for_bit(gpu, f16, transposed):
+    """cache_grow / cache_grow_f16 against numpy: the first `live` positions of
+    every head (every value row, transposed) move to the larger stride, the
+    rest of the destination is untouched (kernels.rs:2144-2240, 3086, 3152)."""
+    kv, hd, cap, new_cap, live = 3, 64, 24, 56, 19
+    src = oracle.seq(kv * cap * hd, 311)
+    fill = oracle.seq(kv * new_cap * hd, 312)
+    if f16:
+        src_b, fill_b = oracle.f32_to_f16(src), oracle.f32_to_f16(fill)
+    else:
+        src_b, fill_b = src.view(np.uint32), fill.view(np.uint32)
+    want = fill_b.copy()
+    if transposed:
+        want.reshape(kv * hd, new_cap)[:, :live] = src_b.reshape(kv * hd, cap)[:, :live]
+    else:
+        want.reshape(kv, new_cap * hd)[:, :live * hd] = src_b.reshape(kv, cap * hd)[:, :live * hd]
+    if f16:
+        d_src, d_dst = up_f16(src), up_f16(fill)
+        gpu.cache_grow_f16(d_src, d_dst, kv, hd, cap, new_cap, live, transposed)
+        assert np.array_equal(down(d_dst).view(np.uint16), want)
+    else:
+        d_src, d_dst = up(src), up(fill)
+        gpu.cache_grow(d_src, d_dst, kv, hd, cap, new_cap, live, transposed)
+        assert np.array_equal(down(d_dst).view(np.uint32), want)
+
+
+def test_rope_cache_writes_the_reference_layout(gpu):
+    """rope_cache_f16 against the oracle: the V row lands at `pos` of V^T as
+    RNE f16 bit for bit; the K row is the oracle's rotation rounded to f16,
+    within one f16 step (the rotation itself matches to ~1e-6 relative, which
+    can move a value across a rounding boundary); q is rotated in place; all
+    other positions are untouched (kernels.rs:1919-2069, 5334)."""
+    heads, kv, hd, cap, pos = 8, 2, 128, 48, 29
+    theta = 500000.0
+    q = oracle.seq(heads * hd, 321)
+    k = oracle.seq(kv * hd, 322)
+    v = oracle.seq(kv * hd, 323)
+    kfill = oracle.seq(kv * cap * hd, 324)
+    vfill = oracle.seq(kv * cap * hd, 325)
+    dq, dk, dvc = up(q), up_f16(kfill), up_f16(vfill)
+    gpu.rope_cache_f16(dq, 0, up(k), 0, up(v), 0, None, heads, kv, hd, theta, pos, dk, dvc, cap)
+    want_v = _ref_scatter(oracle.f32_to_f16(vfill), oracle.f32_to_f16(v).reshape(1, kv, hd), kv, hd, cap, pos, True)
+    assert np.array_equal(down(dvc).view(np.uint16), want_v)
+    kr = oracle.rope(k, 1, kv, hd, theta, pos)
+    want_k = _ref_scatter(oracle.f32_to_f16(kfill), oracle.f32_to_f16(kr).reshape(1, kv, hd), kv, hd, cap, pos, False)
+    got_k = down(dk).view(np.uint16)
+    other = np.ones((kv, cap, hd), bool)
+    other[:, pos, :] = False
+    other = other.ravel()
+    assert np.array_equal(got_k[other], want_k[other])
+    step = np.abs(got_k[~other].astype(np.int32) - want_k[~other].astype(np.int32))
+    assert step.max() <= 1, f"K row off by {step.max()} f16 steps"
+    assert full_scale_err(oracle.rope(q, 1, heads, hd, theta, pos), down(dq)) < 1e-5 + pos * F32EPS

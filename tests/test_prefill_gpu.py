@@ -94,11 +94,15 @@ def test_an_f16_cache_serves_the_same_attention_as_an_f32_one(gpu):
     assert np.abs(a - b).max() / scale < 2e-3
 
 
-@pytest.mark.parametrize("t,heads", [(150, 4), (1500, 20)])
-def test_the_encoder_attention_off_its_rows_is_the_split_path(gpu, t, heads, monkeypatch):
-    # The rows run the staged kernel; the split path is put on it too, so the
-    # two differ only in where K and V are read from.
-    monkeypatch.setenv("LLMTIE_PREFILL_STAGED", "1")
+@pytest.mark.parametrize("staged", [False, True])
+@pytest.mark.parametrize("t,heads", [(150, 4), (1500, 20), (77, 3)])
+def test_the_encoder_attention_off_its_rows_is_the_split_path(gpu, t, heads, staged, monkeypatch):
+    # The rows and the split f32 caches reach the same kernel (the fast one
+    # staging f32 through registers, or with LLMTIE_PREFILL_STAGED the
+    # register-staged fallback), so the two differ only in where K and V are
+    # read from and must agree bit for bit (kernels.rs:4040-4081).
+    if staged:
+        monkeypatch.setenv("LLMTIE_PREFILL_STAGED", "1")
     hd = 64
     d = heads * hd
     scale = float(np.float32(hd) ** np.float32(-0.5))
@@ -114,3 +118,13 @@ def test_the_encoder_attention_off_its_rows_is_the_split_path(gpu, t, heads, mon
     got = down(gpu.flash_attn_rows(up(qkv), t, heads, hd, scale)).view(np.uint16)
     bad = int((want != got).sum())
     assert bad == 0, f"t {t} heads {heads}: {bad} of {want.size} differ"
+
+
+@pytest.mark.skip(reason="removed route: the encoder rows once went through a tiled f16 copy in a cached "
+                         "workspace (f32_to_t16_kernel<64, false>) into flash_fwd_kernel<64, PF_T16>; one MI355X "
+                         "run of it at 1500 rows x 20 heads ended in a GPU memory fault with no cause found in its "
+                         "indexing, ordering or workspace handling. The conversion kernel and the workspace were "
+                         "deleted; the rows are now staged through registers inside the attention kernel "
+                         "(test_the_encoder_attention_off_its_rows_is_the_split_path, test_c4_whisper_encoder).")
+def test_the_removed_tiled_copy_encoder_route():
+    raise AssertionError("this route no longer exists")

@@ -9,10 +9,10 @@ checkpoint here, the same check runs on random weights. The prompt is 250
 tokens so decoding crosses the 256-position cache capacity and exercises the
 growth path. The GPU rounds q and the probabilities to f16 in the prefill
 (the reference's flash arithmetic), so logits agree to ~1e-3 of their scale,
-not bit for bit. The argmax must be identical at every step whose CPU top-two
-margin exceeds twice the measured logit error; a step inside that margin is a
-numerical tie, where the GPU's choice must still be a CPU near-tie. Both
-sides continue from the CPU's token, so a tie cannot cascade.
+not bit for bit. The argmax must be identical at every step (the north
+star's rule); steps whose CPU top-two margin is inside twice the measured
+logit error are counted and printed as near-ties, but they too must agree.
+Both sides continue from the CPU's token.
 """
 import numpy as np
 import pytest
@@ -43,15 +43,12 @@ def test_random_llama_stack_decodes_like_the_cpu(gpu, layout):
         top_c, top_g = int(lc.argmax()), int(lg.argmax())
         srt = np.sort(lc)
         margin = float(srt[-1] - srt[-2])
-        if margin > 2 * err + 1e-6:
-            # not a numerical tie: the argmax must be identical
-            assert top_g == top_c, f"{layout} step {step}: GPU argmax {top_g} != CPU {top_c} (margin {margin:.3g})"
-        else:
-            assert lc[top_g] >= lc[top_c] - 2 * err - 1e-6, f"{layout} step {step}: {top_g} is no CPU near-tie"
+        if margin <= 2 * err + 1e-6:
             ties += 1
+        assert top_g == top_c, f"{layout} step {step}: GPU argmax {top_g} != CPU {top_c} (margin {margin:.3g})"
         ids = [top_c]
+    print(f"{layout}: {ties} of 12 steps had a top-two margin inside twice the logit error", flush=True)
     assert dev.past == cpu.past == 261 and dev.cap == 512
-    assert ties <= 2, f"{layout}: {ties} of 12 steps were numerical ties (random weights should rarely tie)"
 
 
 @pytest.mark.parametrize("layout", ["reference", "tiled"])
@@ -78,7 +75,5 @@ def test_a_gguf_llama_decodes_like_the_cpu(gpu, layout, tmp_path):
         scale = float(np.abs(lc).max())
         err = float(np.abs(lc - lg).max())
         assert err < 5e-3 * scale, f"{layout} step {step}: logit error {err:.3g} of scale {scale:.3g}"
-        srt = np.sort(lc)
-        if float(srt[-1] - srt[-2]) > 2 * err + 1e-6:
-            assert int(lg.argmax()) == int(lc.argmax()), f"{layout} step {step}"
+        assert int(lg.argmax()) == int(lc.argmax()), f"{layout} step {step}"
         ids = [int(lc.argmax())]

@@ -9,8 +9,6 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <mutex>
-#include <vector>
 
 #include "../../include/llmtie_hip.h"
 #include "decode.h"
@@ -124,71 +122,6 @@ int pick_nqt(size_t tq, size_t heads, int gb) {
     return 1;
 }
 
-// Workspace for the tiled f16 copy of f32 K/V: one grow-only buffer per
-// (device, stream), so calls ordered on a stream share it and concurrent
-// streams never do. A buffer is never freed or reallocated in place (a
-// captured HIP graph may hold its address): growth allocates a larger one
-// and keeps the old alive until the process ends. Growth is not possible
-// while the stream is capturing; the caller then falls back to a
-// stream-ordered allocation inside the graph.
-struct Workspace {
-    int device;
-    hipStream_t stream;
-    void* ptr;
-    size_t bytes;
-};
-std::mutex ws_mutex;
-std::vector<Workspace> ws_list;
-
-void* cached_workspace(hipStream_t st, size_t bytes) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lock(ws_mutex);
-    for (Workspace& w : ws_list)
-        if (w.device == dev && w.stream == st && w.bytes >= bytes) return w.ptr;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    void* p = nullptr;
-    const size_t want = std::max<size_t>(bytes, (size_t)1 << 20);
-    if (hipMalloc(&p, want) != hipSuccess) return nullptr;
-    for (Workspace& w : ws_list)
-        if (w.device == dev && w.stream == st) {
-            w.ptr = p;  // the old buffer stays allocated (see above)
-            w.bytes = want;
-            return p;
-        }
-    ws_list.push_back(Workspace{dev, st, p, want});
-    return p;
-}
-
-// f32 K/V go through the f16 fast kernel via a tiled f16 copy in a
-// workspace; the staged kernel is the fallback for a non-positive score
-// scale, which the fast kernel does not take.
-int prefill_via_t16(const char* what, hipStream_t st, PrefillArgs a, int hd, int nqt, const float* k, long khs,
-                    long kps, const float* v, long vhs, long vps, long vds, int fallback_kind) {
-    if (!(a.scale_q || a.scale > 0.0f) || getenv("LLMTIE_PREFILL_STAGED"))
-        return launched(what, launch_prefill(hd, fallback_kind, nqt, a, st));
-    const int nkeys = a.past + a.tq;
-    const size_t bytes = (size_t)a.kv_heads * tiled_nblk(nkeys) * 64 * hd * 2;
-    void* ws = cached_workspace(st, bytes);
-    const bool ordered = ws == nullptr;
-    if (ordered) {
-        hipError_t e = hipMallocAsync(&ws, bytes, st);
-        if (e != hipSuccess) return driver("hipMallocAsync", e);
-    }
-    hipError_t e = launch_f32_to_t16(k, khs, kps, v, vhs, vps, vds, static_cast<uint16_t*>(ws), a.kv_heads, hd,
-                                     nkeys, st);
-    if (e == hipSuccess) {
-        a.k = ws;
-        a.v = nullptr;
-        a.cap = nkeys;
-        e = launch_prefill(hd, PF_T16, nqt, a, st);
-    }
-    const hipError_t ef = ordered ? hipFreeAsync(ws, st) : hipSuccess;
-    if (e != hipSuccess) return driver(what, e);
-    return launched("hipFreeAsync", ef);
-}
-
 int prefill_common(void* stream, int kind, const float* q, size_t q_len, const void* k, size_t k_len, const void* v,
                    size_t v_len, float* out, size_t out_len, size_t tq, size_t past, size_t heads, size_t kv_heads,
                    size_t hd, size_t cap, float scale, int causal) {
@@ -222,12 +155,6 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
     a.scale_q = 0;
     a.v_bytes = v_len * (kind == PF_F32 ? 4 : 2);
     const int nqt = pick_nqt(tq, heads, gb);
-    if (kind == PF_F32) {
-        const float* kf = static_cast<const float*>(k);
-        const float* vf = static_cast<const float*>(v);
-        return prefill_via_t16("flash_attn", S(stream), a, (int)hd, nqt, kf, (long)(cap * hd), (long)hd, vf,
-                               (long)(hd * cap), 1, (long)cap, PF_F32);
-    }
     return launched("flash_attn", launch_prefill((int)hd, kind, nqt, a, S(stream)));
 }
 
@@ -462,11 +389,8 @@ int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint1
     a.os = (int)d;
     a.scale_q = 1;
     a.out_f16 = 1;
-    // The staged kernel reads the stacked f32 rows directly. The faster
-    // route through a tiled f16 copy (prefill_via_t16 with the stacked-rows
-    // conversion) is switched off: one MI355X run of it at 1500 rows x 20
-    // heads ended in a GPU memory fault, identical code and inputs had passed
-    // before, and no cause has been found in its indexing or ordering.
+    // The stacked f32 rows are read in place: the attention kernel stages
+    // them through registers into its f16 LDS tiles (no copy, no workspace).
     return launched("flash_attn_rows", launch_prefill(64, PF_ROWS, pick_nqt(t, heads, 1), a, S(stream)));
 }
 

@@ -37,13 +37,6 @@ struct PrefillArgs {
     int xcd, nrb;
 };
 
-// f32 K/V (a cache or the column blocks of stacked rows) -> the tiled f16
-// layout of kvlayout.h, `nkeys` keys of `kv` heads; element (head h, key p,
-// dim d) of K is at k[h*khs + p*kps + d] and of V at v[h*vhs + p*vps + d*vds].
-// Positions from nkeys to the end of the last block are written as zeros.
-hipError_t launch_f32_to_t16(const float* k, long khs, long kps, const float* v, long vhs, long vps, long vds,
-                             uint16_t* dst, int kv, int hd, int nkeys, hipStream_t st);
-
 // nqt: 16-query tiles per wave (1, 2 or 4).
 hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st);
 

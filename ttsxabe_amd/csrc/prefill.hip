@@ -405,7 +405,11 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
 // one tile that reaches past ktot they are zeroed in LDS before use.
 template <int HD, int KIND, int NQT>
 __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
-    static_assert(KIND == PF_F16 || KIND == PF_T16, "f16 caches only");
+    static_assert(KIND == PF_F16 || KIND == PF_T16 || KIND == PF_F32 || KIND == PF_ROWS, "unknown source");
+    // f32 sources (the f32 cache, the stacked encoder rows) are staged through
+    // registers: loaded as f32, rounded to f16 and written to LDS in the same
+    // fragment order the direct-to-LDS kinds produce.
+    constexpr bool STAGED = KIND == PF_F32 || KIND == PF_ROWS;
     constexpr int NS = HD / 32;
     constexpr int NT = HD / 16;
     constexpr int QPW = 16 * NQT;
@@ -447,12 +451,77 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     const __amdgpu_buffer_rsrc_t rv =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.v), 0, (int)(uint32_t)a.v_bytes, 0x00020000);
 
+    // Register staging (STAGED kinds). Fragment f = wave + PW * i of a tile,
+    // lane (col, grp): K fragment (half, T, s) is key 32*half + 8*(col/4) +
+    // 4T + col%4, dims 32s + 8grp .. +7 (two float4 of one K row); V fragment
+    // (half, t) is dim 16t + col, keys 32*half + 8grp .. +7 (two float4 of
+    // one V^T row of the f32 cache, or one float from each of 8 stacked
+    // rows). K rows past the live keys are clamped to the last live one (their
+    // scores are masked); V entries past them are zero, so no tail pass is
+    // needed. Every address stays below key ktot - 1 of its head.
+    const float* kf32 = static_cast<const float*>(a.k);
+    const float* vf32 = static_cast<const float*>(a.v);
+    const size_t skb = KIND == PF_ROWS ? (size_t)kh * HD : (size_t)kh * a.cap * HD;  // K: head base
+    const size_t skr = KIND == PF_ROWS ? (size_t)a.kvs : (size_t)HD;                 // K: row stride
+    const size_t svb = KIND == PF_ROWS ? (size_t)kh * HD : (size_t)kh * HD * a.cap;  // V: head base
+    const bool vvec = KIND == PF_F32 && a.cap % 4 == 0;  // V^T rows 16-byte aligned
+    constexpr int NSR = STAGED ? NF : 1;
+    float4 sr[NSR][2];
+    auto stage_load = [&](int kv0) {
+        if constexpr (STAGED) {
+#pragma unroll
+            for (int i = 0; i < NF; ++i) {
+                const int f = wave + PW * i;
+                if (f < KF) {
+                    const int hf = f / (2 * NS), T = (f / NS) & 1, s = f % NS;
+                    const int key = min(kv0 + 32 * hf + 8 * (col >> 2) + 4 * T + (col & 3), ktot - 1);
+                    const float4* p = reinterpret_cast<const float4*>(kf32 + skb + (size_t)key * skr + 32 * s + 8 * grp);
+                    sr[i][0] = p[0];
+                    sr[i][1] = p[1];
+                } else {
+                    const int fv = f - KF, hf = fv / NT, t = fv % NT;
+                    const int d = 16 * t + col, k0 = kv0 + 32 * hf + 8 * grp;
+                    float x[8];
+                    if (KIND == PF_F32 && vvec && k0 + 8 <= ktot) {
+                        const float4* p = reinterpret_cast<const float4*>(vf32 + svb + (size_t)d * a.cap + k0);
+                        sr[i][0] = p[0];
+                        sr[i][1] = p[1];
+                        continue;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int key = min(k0 + j, ktot - 1);
+                        const size_t at = KIND == PF_ROWS ? svb + (size_t)key * a.kvs + d : svb + (size_t)d * a.cap + key;
+                        x[j] = k0 + j < ktot ? vf32[at] : 0.0f;
+                    }
+                    sr[i][0] = make_float4(x[0], x[1], x[2], x[3]);
+                    sr[i][1] = make_float4(x[4], x[5], x[6], x[7]);
+                }
+            }
+        }
+    };
+    auto stage_store = [&](half_t* dst) {
+        if constexpr (STAGED) {
+#pragma unroll
+            for (int i = 0; i < NF; ++i) {
+                const int f = wave + PW * i;
+                const float4 x0 = sr[i][0], x1 = sr[i][1];
+                half8 y;
+                y[0] = to_h(x0.x); y[1] = to_h(x0.y); y[2] = to_h(x0.z); y[3] = to_h(x0.w);
+                y[4] = to_h(x1.x); y[5] = to_h(x1.y); y[6] = to_h(x1.z); y[7] = to_h(x1.w);
+                reinterpret_cast<half8*>(dst + f * FH)[lane] = y;
+            }
+        }
+    };
+
     auto issue = [&](int kv0, half_t* dst) {
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int f = wave + PW * i;
             half_t* l = dst + f * FH;
-            if constexpr (KIND == PF_T16) {
+            if constexpr (STAGED) {
+                (void)l;
+            } else if constexpr (KIND == PF_T16) {
                 const int hf = f < KF ? f / (2 * NS) : (f - KF) / NT;
                 const int b = min((kv0 >> 5) + hf, lastb);
                 const int in = f < KF ? (f % (2 * NS)) * FH : 32 * HD + ((f - KF) % NT) * FH;
@@ -477,7 +546,11 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     // The first tile's loads go out before the query's (the query's first
     // use waits for every load issued before it, tile loads included: the
     // compiler does not count LDS-DMA loads in order).
-    if (kend > 0) issue(0, t0);
+    if constexpr (STAGED) {
+        if (kend > 0) stage_load(0);
+    } else {
+        if (kend > 0) issue(0, t0);
+    }
     const float qsc = a.scale_q ? a.scale : 1.0f;
     float4 qx[NQT][NS][2];
 #pragma unroll
@@ -653,9 +726,35 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
             tile(cur, kv0, std::false_type{});
     };
 
-    for (int kv0 = 0; kv0 < kend; kv0 += 2 * KT) {
-        step(t0, t1, kv0);
-        if (kv0 + KT < kend) step(t1, t0, kv0 + KT);
+    // Staged kinds: tile j is in LDS buffer `cur` when the barrier passes;
+    // tile j + 1's f32 loads are in flight in registers while tile j is
+    // computed, then rounded and written to `nxt`, which every wave finished
+    // reading before that barrier.
+    auto step_staged = [&](half_t* cur, half_t* nxt, int kv0) {
+        __syncthreads();
+        const bool more = kv0 + KT < kend;
+        if (more) stage_load(kv0 + KT);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kv0 <= wlim) {
+            if (kv0 + KT - 1 > wall)
+                tile(cur, kv0, std::true_type{});
+            else
+                tile(cur, kv0, std::false_type{});
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) stage_store(nxt);
+    };
+    if constexpr (STAGED) {
+        if (kend > 0) stage_store(t0);
+        for (int kv0 = 0; kv0 < kend; kv0 += 2 * KT) {
+            step_staged(t0, t1, kv0);
+            if (kv0 + KT < kend) step_staged(t1, t0, kv0 + KT);
+        }
+    } else {
+        for (int kv0 = 0; kv0 < kend; kv0 += 2 * KT) {
+            step(t0, t1, kv0);
+            if (kv0 + KT < kend) step(t1, t0, kv0 + KT);
+        }
     }
 
     // O / l, stored: lane writes dims 16t + 4grp + 0..3 of query p0 + 16u + col.
@@ -681,82 +780,6 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     }
 }
 
-// f32 K/V -> the tiled f16 layout, one thread per 16-byte output chunk (the
-// layout is [head][block][fragment][lane], so consecutive threads write
-// consecutive chunks). K chunk (T, s, lane) holds key 8*(col/4) + 4T + col%4,
-// dims 32s + 8grp .. +7: 32 contiguous bytes of one K row. V chunk (t, lane)
-// holds dim 16t + col, keys 8grp .. +7: 32 contiguous bytes of one V^T row
-// (VKEY, the f32 cache), or one float from each of 8 V rows (stacked rows,
-// consecutive lanes reading consecutive dims). Keys past nkeys are zeros;
-// f32 -> f16 rounds to nearest even, as the kernels' own staging does.
-template <int HD, bool VKEY>
-__global__ __launch_bounds__(256) void f32_to_t16_kernel(const float* __restrict__ k, long khs, long kps,
-                                                         const float* __restrict__ v, long vhs, long vps, long vds,
-                                                         half_t* __restrict__ dst, int nkeys, int nblk, long nchunk) {
-    constexpr int NS = HD / 32, NT = HD / 16, CPB = (2 * NS + NT) * 64;  // chunks per block
-    // Work item i runs (block, head) = (i / kv, i % kv): workgroups running
-    // together read the same source rows (every head's columns of one
-    // 32-key block) rather than one head's columns of rows spread over the
-    // whole tensor. The chunk written is at its layout place, [head][block].
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= nchunk) return;
-    const long kvh = nchunk / ((long)nblk * CPB);
-    const long bh = i / CPB;
-    const int w = (int)(i % CPB), f = w / 64, lane = w % 64, col = lane & 15, grp = lane >> 4;
-    const int h = (int)(bh % kvh), b = (int)(bh / kvh);
-    const long c = ((long)h * nblk + b) * CPB + w;
-    float x[8];
-    if (f < 2 * NS) {
-        const int T = f / NS, s = f % NS;
-        const int key = 32 * b + 8 * (col >> 2) + 4 * T + (col & 3);
-        if (key < nkeys) {
-            const float4* p = reinterpret_cast<const float4*>(k + h * khs + (long)key * kps + 32 * s + 8 * grp);
-            const float4 a0 = p[0], a1 = p[1];
-            x[0] = a0.x; x[1] = a0.y; x[2] = a0.z; x[3] = a0.w; x[4] = a1.x; x[5] = a1.y; x[6] = a1.z; x[7] = a1.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = 0.0f;
-        }
-    } else {
-        const int d = 16 * (f - 2 * NS) + col, k0 = 32 * b + 8 * grp;
-        if constexpr (VKEY) {
-            const float* p = v + h * vhs + (long)d * vds + k0;
-            if (k0 + 8 <= nkeys) {
-                const float4 a0 = reinterpret_cast<const float4*>(p)[0], a1 = reinterpret_cast<const float4*>(p)[1];
-                x[0] = a0.x; x[1] = a0.y; x[2] = a0.z; x[3] = a0.w; x[4] = a1.x; x[5] = a1.y; x[6] = a1.z; x[7] = a1.w;
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = k0 + j < nkeys ? p[j] : 0.0f;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = k0 + j < nkeys ? v[h * vhs + (long)(k0 + j) * vps + d] : 0.0f;
-        }
-    }
-    half8 y;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = to_h(x[j]);
-    reinterpret_cast<half8*>(dst)[c] = y;
-}
-
-hipError_t launch_f32_to_t16(const float* k, long khs, long kps, const float* v, long vhs, long vps, long vds,
-                             uint16_t* dst, int kv, int hd, int nkeys, hipStream_t st) {
-    const int nblk = tiled_nblk(nkeys);
-    const long nchunk = (long)kv * nblk * (hd / 8) * 64;  // chunks per block: 2 * hd/32 (K) + hd/16 (V)
-    const dim3 grid((unsigned)((nchunk + 255) / 256));
-    half_t* d = reinterpret_cast<half_t*>(dst);
-    const bool vkey = vps == 1;
-#define CV(HD, VK)                                                                                      \
-    if (hd == HD && vkey == VK) {                                                                       \
-        hipLaunchKernelGGL((f32_to_t16_kernel<HD, VK>), grid, dim3(256), 0, st, k, khs, kps, v, vhs, vps, vds, d, \
-                           nkeys, nblk, nchunk);                                                        \
-        return hipGetLastError();                                                                       \
-    }
-    CV(64, false) CV(64, true) CV(128, false) CV(128, true)
-#undef CV
-    return hipErrorInvalidValue;
-}
-
 hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st) {
     const int pb = 16 * nqt * (PW / a.gb);
     dim3 grid((a.tq + pb - 1) / pb, a.heads / a.gb), block(PT);
@@ -769,7 +792,11 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
     // The f16 caches take the direct-to-LDS kernel when the V cache is
     // addressable by a 32-bit buffer offset (always, for the tiled cache).
     // (It keeps the raw-score max, so it needs a positive score scale.)
-    const bool fast = (kind == PF_T16 || (kind == PF_F16 && a.v_bytes <= 0xffffffffull)) &&
+    // The f32 sources take it through register staging when K and V are
+    // 16-byte aligned (rows: a row stride of whole float4s).
+    const bool al16 = ((reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v)) & 15) == 0;
+    const bool f32ok = (kind == PF_F32 && al16) || (kind == PF_ROWS && al16 && a.kvs % 4 == 0);
+    const bool fast = (kind == PF_T16 || (kind == PF_F16 && a.v_bytes <= 0xffffffffull) || f32ok) &&
                       (a.scale_q || a.scale > 0.0f) && !getenv("LLMTIE_PREFILL_STAGED");
     if (fast) {
         PrefillArgs b = a;
@@ -784,6 +811,8 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
     }
         F(64, PF_F16, 1) F(64, PF_F16, 2) F(128, PF_F16, 1) F(128, PF_F16, 2)
         F(64, PF_T16, 1) F(64, PF_T16, 2) F(128, PF_T16, 1) F(128, PF_T16, 2)
+        F(64, PF_F32, 1) F(64, PF_F32, 2) F(128, PF_F32, 1) F(128, PF_F32, 2)
+        F(64, PF_ROWS, 1) F(64, PF_ROWS, 2)
 #undef F
     }
     LK(64, PF_F16) LK(128, PF_F16) LK(64, PF_F32) LK(128, PF_F32) LK(64, PF_ROWS) LK(64, PF_T16) LK(128, PF_T16)
