@@ -51,7 +51,10 @@ typedef enum llmtie_status {
     LLMTIE_ODD_HEAD_DIM = 7,          /* OddHeadDim{head_dim}             error.rs:210 */
     LLMTIE_DRIVER = 8,                /* Driver{what, source}             error.rs:281 */
     LLMTIE_NO_DEVICE = 9,             /* NoDevice(String)                 error.rs:242 */
-    LLMTIE_INVALID_ARGUMENT = 10      /* a null pointer where a buffer is required (no reference twin) */
+    LLMTIE_INVALID_ARGUMENT = 10,     /* a null pointer where a buffer is required (no reference twin) */
+    LLMTIE_SCRATCH_GROWTH_IN_CAPTURE = 11 /* a decode scratch would have to grow while its stream captures a
+                                           * graph (no reference twin: the reference does not capture);
+                                           * fields: partial floats needed, held, counters needed, held */
 } llmtie_status;
 
 /* The last error raised on the calling thread: the status, up to four numeric
@@ -70,7 +73,14 @@ const char* llmtie_version(void);
 
 /* Opaque decode scratch: split partials and arrival counters, grown on demand
  * and owned by the caller. Replaces `DecodeScratch::new()` (device.rs:219).
- * Its counters start at zero and every call leaves them at zero. */
+ * Its counters start at zero and every call leaves them at zero.
+ * Graphs: a call captured into a HIP graph records the scratch's buffers.
+ * Growth never frees a buffer: the replaced one stays allocated until
+ * llmtie_decode_scratch_free (the 64 most recent; an older one is released
+ * after a device synchronisation), so an earlier graph keeps replaying
+ * correctly. Growth is refused while the stream is capturing
+ * (LLMTIE_SCRATCH_GROWTH_IN_CAPTURE): make one eager call of the largest shape
+ * first. Freeing the scratch invalidates every graph that used it. */
 typedef struct llmtie_decode_scratch llmtie_decode_scratch;
 llmtie_decode_scratch* llmtie_decode_scratch_new(void);
 void llmtie_decode_scratch_free(llmtie_decode_scratch* s);

@@ -2,8 +2,8 @@
 the program's own eager work and synchronisations between replays, must give
 the eager result bit for bit. Covers the decode's split hand-off (arrival
 counters left at zero by every call, so a replay starts clean), the two-phase
-merge, the prefill, and the f32 prefill's stream-ordered workspace
-(allocated and freed inside the graph)."""
+merge, the prefill (f16 caches, and the f32 sources staged inside the
+kernel), and the decode scratch's growth around a captured graph."""
 import os
 
 import numpy as np
@@ -69,3 +69,42 @@ def test_encoder_rows_graph_replays(gpu):
     t, heads, hd = 1500, 20, 64
     qkv = up(oracle.seq(t * 3 * heads * hd, 7))
     _replays_match(lambda: [gpu.flash_attn_rows(qkv, t, heads, hd, 0.125)])
+
+
+def test_scratch_growth_keeps_an_earlier_graph_valid(gpu):
+    """A graph captured with a small scratch, then an eager call that grows
+    the scratch: the old buffers stay allocated, so the old graph still
+    replays to its eager result; growth inside a capture is refused by name."""
+    from ttsxabe_amd.gpu import DecodeScratch, ScratchGrowthInCapture
+    heads, kv, hd, cap = 32, 8, 128, 8192
+    q = up(oracle.seq(heads * hd, 21))
+    k = up_f16(oracle.seq(kv * cap * hd, 22))
+    v = up_f16(oracle.seq(kv * cap * hd, 23))
+    s = DecodeScratch()
+    small = lambda: [gpu.attn_decode_f16(q, k, v, heads, kv, hd, 1000, cap, 0.088, False, s)]
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        eager = [t.clone() for t in small()]
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            outs = small()
+        # a larger call on a fresh scratch inside a capture: refused, nothing launched
+        g2 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g2, stream=st):
+            with pytest.raises(ScratchGrowthInCapture):
+                gpu.attn_decode_f16(q, k, v, heads, kv, hd, 8000, cap, 0.088, False, DecodeScratch())
+            keep = q * 2.0  # the graph is not empty
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    # grow the scratch eagerly: a longer context, then twice the kv heads
+    for tk, h, kvh in ((8000, heads, kv), (2000, 64, 16)):
+        kk = up_f16(oracle.seq(kvh * cap * hd, 24))
+        gpu.attn_decode_f16(up(oracle.seq(h * hd, 25)), kk, kk, h, kvh, hd, tk, cap, 0.088, False, s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        outs[0].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(eager[0], outs[0]), f"replay {i} after growth differs"

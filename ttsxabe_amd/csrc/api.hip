@@ -78,6 +78,10 @@ struct llmtie_decode_scratch {
     unsigned* ctr = nullptr;
     size_t ctr_cap = 0;   // counters
     int device = -1;
+    // Buffers replaced by growth. A HIP graph captured with the scratch keeps
+    // their addresses, so they stay allocated until the scratch is freed.
+    void* retired[64] = {nullptr};
+    int nretired = 0;
 };
 
 extern "C" {
@@ -95,6 +99,7 @@ void llmtie_decode_scratch_free(llmtie_decode_scratch* s) {
     if (!s) return;
     if (s->part) (void)hipFree(s->part);
     if (s->ctr) (void)hipFree(s->ctr);
+    for (int i = 0; i < s->nretired; ++i) (void)hipFree(s->retired[i]);
     delete s;
 }
 
@@ -108,7 +113,7 @@ namespace {
 
 // 16-query tiles per wave: the most that still leaves about two workgroups
 // per CU (256 CUs), so short prefills spread over the whole chip.
-int pick_nqt(size_t tq, size_t heads, int gb) {
+int pick_nqt(size_t tq, size_t heads, int gb, bool staged = false) {
     if (const char* e = getenv("LLMTIE_PREFILL_NQT")) {
         const int v = atoi(e);
         if (v == 1 || v == 2 || v == 4) return v;
@@ -118,7 +123,12 @@ int pick_nqt(size_t tq, size_t heads, int gb) {
     // once the launch still has >= 512 workgroups; below that, one tile per
     // wave, for the parallelism.
     const size_t pb2 = 32 * (4 / gb);
-    if (((tq + pb2 - 1) / pb2) * (heads / gb) >= 512) return 2;
+    const size_t wg2 = ((tq + pb2 - 1) / pb2) * (heads / gb);
+    if (wg2 >= 512) return 2;
+    // f32 sources staged through registers: two tiles per wave halve the
+    // staging per query row, which wins down to about one workgroup per CU
+    // (C4 encoder, 240 workgroups: 38.7 vs 40.1 us).
+    if (staged && wg2 >= 192) return 2;
     return 1;
 }
 
@@ -154,7 +164,7 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
     a.os = (int)(heads * hd);
     a.scale_q = 0;
     a.v_bytes = v_len * (kind == PF_F32 ? 4 : 2);
-    const int nqt = pick_nqt(tq, heads, gb);
+    const int nqt = pick_nqt(tq, heads, gb, kind == PF_F32);
     return launched("flash_attn", launch_prefill((int)hd, kind, nqt, a, S(stream)));
 }
 
@@ -217,11 +227,13 @@ int two_phase_merge(int splits, size_t units) {
 // so no line is shared by two heads' partials.
 size_t ml_stride(int splits, size_t group) { return ((size_t)splits * group * 2 + 63) / 64 * 64; }
 
-// Whether a host-planned in-launch merge keeps every head on one XCD: each
-// XCD's run of (launch / 8) items (the dispatcher deals workgroups to the
-// eight XCDs of gfx950 round-robin) holds whole heads. A partitioned device
-// with 4, 2 or 1 XCDs still groups them: workgroups L = x mod 8 then share
-// XCD x mod (its XCD count).
+// Whether a host-planned in-launch merge keeps every head on one XCD: the
+// dispatcher deals a launch's workgroups to the eight XCDs of gfx950 in
+// turn, so workgroups L and L + 8k share an XCD (which XCD a launch starts on
+// varies with what ran before; a partitioned device with fewer XCDs still
+// groups them). The plan runs workgroup L on item (L % 8) * (launch / 8) +
+// L / 8, so each XCD's run of items must hold whole heads. The kernel checks
+// the grouping itself (the arrival counter sums the XCC ids).
 int xcd_local(int splits, size_t units, int two_phase) {
     if (const char* e = getenv("LLMTIE_DECODE_XCD")) {
         if (!atoi(e)) return 0;
@@ -231,14 +243,43 @@ int xcd_local(int splits, size_t units, int two_phase) {
     return (total / 8) % (size_t)splits == 0 ? 1 : 0;
 }
 
+// A buffer the scratch no longer uses. It is kept allocated (a graph
+// captured earlier may still read it) until the scratch is freed; past 64
+// retirements the oldest is released after the device has drained.
+int retire(llmtie_decode_scratch* s, void* p) {
+    if (!p) return LLMTIE_OK;
+    if (s->nretired == 64) {
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return driver("hipDeviceSynchronize", e);
+        (void)hipFree(s->retired[0]);
+        memmove(s->retired, s->retired + 1, 63 * sizeof(void*));
+        s->nretired = 63;
+    }
+    s->retired[s->nretired++] = p;
+    return LLMTIE_OK;
+}
+
 int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hipStream_t st) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return driver("hipGetDevice", e);
-    if (s->device != dev) {
+    const bool swap = s->device != dev;
+    const bool grow = swap || s->part_cap < part_floats || s->ctr_cap < ctrs;
+    if (!grow) return LLMTIE_OK;
+    // Allocating inside a stream capture would put the allocation into the
+    // graph (or fail); the caller makes one eager call first instead.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) return driver("hipStreamIsCapturing", e);
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(LLMTIE_SCRATCH_GROWTH_IN_CAPTURE, part_floats, s->part_cap, ctrs, s->ctr_cap,
+                    "the decode scratch must grow to %zu partial floats and %zu counters while the stream is "
+                    "capturing a graph; make one call of this shape before capturing",
+                    part_floats, ctrs);
+    int r;
+    if (swap) {
         // A scratch follows the device it is used on; switching starts over.
-        if (s->part) (void)hipFree(s->part);
-        if (s->ctr) (void)hipFree(s->ctr);
+        if ((r = retire(s, s->part)) != LLMTIE_OK || (r = retire(s, s->ctr)) != LLMTIE_OK) return r;
         s->part = nullptr;
         s->ctr = nullptr;
         s->part_cap = s->ctr_cap = 0;
@@ -247,25 +288,31 @@ int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hi
     if (s->part_cap < part_floats) {
         size_t want = 1024;
         while (want < part_floats) want <<= 1;
-        if (s->part) (void)hipFree(s->part);
-        s->part = nullptr;
-        s->part_cap = 0;
-        e = hipMalloc(&s->part, want * sizeof(float));
+        float* p = nullptr;
+        e = hipMalloc(&p, want * sizeof(float));
         if (e != hipSuccess) return driver("allocating", e);
+        if ((r = retire(s, s->part)) != LLMTIE_OK) {
+            (void)hipFree(p);
+            return r;
+        }
+        s->part = p;
         s->part_cap = want;
     }
     if (s->ctr_cap < ctrs) {
         size_t want = 64;
         while (want < ctrs) want <<= 1;
-        if (s->ctr) (void)hipFree(s->ctr);
-        s->ctr = nullptr;
-        s->ctr_cap = 0;
-        e = hipMalloc(&s->ctr, want * sizeof(unsigned));
+        unsigned* c = nullptr;
+        e = hipMalloc(&c, want * sizeof(unsigned));
         if (e != hipSuccess) return driver("allocating", e);
         // Zeroed by a kernel on the caller's stream (a memset node inside a
         // captured graph is not to be relied on).
-        e = launch_fill_u32(s->ctr, want, 0u, st);
-        if (e != hipSuccess) return driver("zeroing", e);
+        e = launch_fill_u32(c, want, 0u, st);
+        if (e != hipSuccess) {
+            (void)hipFree(c);
+            return driver("zeroing", e);
+        }
+        if ((r = retire(s, s->ctr)) != LLMTIE_OK) return r;
+        s->ctr = c;
         s->ctr_cap = want;
     }
     return LLMTIE_OK;
@@ -339,6 +386,7 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     a.ml_stride = (long)mls;
     a.two_phase = two_phase_merge(splits, kv_heads);
     a.xcd = xcd_local(splits, kv_heads, a.two_phase);
+    a.xcd_fake = getenv("LLMTIE_DECODE_XCD_FAKE") ? 1 : 0;
     return launched("attn_decode", launch_decode((int)hd, kind, a, (int)kv_heads, 1, S(stream)));
 }
 
@@ -391,7 +439,7 @@ int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint1
     a.out_f16 = 1;
     // The stacked f32 rows are read in place: the attention kernel stages
     // them through registers into its f16 LDS tiles (no copy, no workspace).
-    return launched("flash_attn_rows", launch_prefill(64, PF_ROWS, pick_nqt(t, heads, 1), a, S(stream)));
+    return launched("flash_attn_rows", launch_prefill(64, PF_ROWS, pick_nqt(t, heads, 1, true), a, S(stream)));
 }
 
 int llmtie_attn_decode_f16(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
@@ -489,6 +537,7 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     a.ml_stride = (long)mls;
     a.two_phase = sk ? 0 : two_phase_merge(splits, kv_heads * nseq);
     a.xcd = sk ? 0 : xcd_local(splits, kv_heads * nseq, a.two_phase);
+    a.xcd_fake = getenv("LLMTIE_DECODE_XCD_FAKE") ? 1 : 0;
     a.sk = sk ? 1 : 0;
     a.nseq = (int)nseq;
     a.items = items;

@@ -52,7 +52,13 @@ struct DecodeArgs {
     // to the XCDs round-robin and the host sets xcd only when every XCD's run
     // of items holds whole heads, so a head's splits, partials and merge all
     // stay in one XCD's L2: plain partial stores, L2 reads in the merge.
+    // The dispatcher is only relied on for workgroups L and L + 8k sharing an
+    // XCD (which one a launch starts on varies with what ran before). Each
+    // workgroup adds its hardware XCC id to the head's arrival counter, so
+    // the merging workgroup sees whether the head really stayed on one XCD;
+    // if not, the head's context is written as NaN, never silently wrong.
     int xcd;
+    int xcd_fake;  // tests only: report XCC id (L / 8) % 8 instead of the real one
 };
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);

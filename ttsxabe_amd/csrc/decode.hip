@@ -556,6 +556,22 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
 }
 
 
+// The hardware id of the XCD this wave runs on (HW_REG_XCC_ID, bits 3:0).
+__device__ __forceinline__ unsigned xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15u; }
+
+// Arrival counter (64 bits, on its own 256-byte line): bits 0-15 count the
+// arrivals, bits 16-31 sum the arriving workgroups' XCC ids x and bits 32-47
+// their squares. The n arrivals shared one XCD exactly when n * sum(x^2) =
+// sum(x)^2 (Cauchy-Schwarz equality). Ids are < 16 and splits <= 256, so no
+// field overflows into the next.
+__device__ __forceinline__ unsigned long long arrival(unsigned x) {
+    return 1ull | ((unsigned long long)x << 16) | ((unsigned long long)(x * x) << 32);
+}
+__device__ __forceinline__ bool one_xcd(unsigned long long c) {
+    const unsigned long long n = c & 0xffff, s1 = (c >> 16) & 0xffff, s2 = (c >> 32) & 0xffff;
+    return n * s2 == s1 * s1;
+}
+
 template <int HD, int KIND, int VA>
 __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel(DecodeArgs a) {
     constexpr int NS = HD / 32;
@@ -802,17 +818,35 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    unsigned* ctr = a.ctr + head * CTR_STRIDE;
+    unsigned long long* ctr = reinterpret_cast<unsigned long long*>(a.ctr + head * CTR_STRIDE);
     if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = prev == (unsigned)(nsplit - 1);
+        const unsigned x = a.xcd_fake ? (blockIdx.x / 8) % 8 : xcc_id();
+        const unsigned long long add = arrival(x);
+        const unsigned long long prev = __hip_atomic_fetch_add(ctr, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // 1: the last arrival, every partial readable here; 2: the last
+        // arrival of an XCD-local head whose workgroups did not share an XCD.
+        last = (prev & 0xffff) != (unsigned long long)(nsplit - 1) ? 0 : (a.xcd && !one_xcd(prev + add)) ? 2 : 1;
     }
     __syncthreads();
     if (!last) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (last == 2) {
+        // Partials stored into another XCD's L2 are not visible here: the
+        // head's context is reported as NaN (its twin with NaN scales).
+        for (int e = tid; e < n; e += DT) {
+            const size_t idx = (size_t)h * group * HD + e;
+            out[idx] = __builtin_nanf("");
+            if (tc) {
+                tc[idx] = 0;
+                if ((e & 31) == 0) ts[idx >> 5] = __builtin_nanf("");
+            }
+        }
+        if (tid == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     if (loc) merge_head<HD, AUX_XCD>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
     else merge_head<HD, AUX_AGENT>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
-    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The merge of one head's splits as a launch of its own, after a two-phase

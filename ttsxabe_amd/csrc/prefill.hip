@@ -467,11 +467,29 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     const bool vvec = KIND == PF_F32 && a.cap % 4 == 0;  // V^T rows 16-byte aligned
     constexpr int NSR = STAGED ? NF : 1;
     float4 sr[NSR][2];
+    // Stacked rows: V is [key][dim], so a thread takes 4 dims x 4 keys
+    // (one float4 from each of 4 rows; 16 threads cover one 256-byte row
+    // segment) instead of one fragment chunk, and writes each dim's 4 keys
+    // as one 8-byte half of a chunk. The V fragments are the wave's last
+    // NF - KF / PW staging slots.
+    static_assert(KIND != PF_ROWS || (HD == 64 && KF % PW == 0 && VF * 64 * 8 == PT * 16), "rows: hd 64");
+    constexpr int KI = KF / PW;  // staging slots holding K fragments
+    const int rdq = tid & 15, rkq = tid >> 4;  // rows V: dims 4*rdq .. +3, keys 4*rkq .. +3
     auto stage_load = [&](int kv0) {
+        if constexpr (KIND == PF_ROWS) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int key = kv0 + 4 * rkq + u;
+                const float4 x = *reinterpret_cast<const float4*>(vf32 + svb + (size_t)min(key, ktot - 1) * a.kvs +
+                                                                  4 * rdq);
+                sr[KI + u / 2][u % 2] = key < ktot ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
         if constexpr (STAGED) {
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
                 const int f = wave + PW * i;
+                if (KIND == PF_ROWS && i >= KI) continue;
                 if (f < KF) {
                     const int hf = f / (2 * NS), T = (f / NS) & 1, s = f % NS;
                     const int key = min(kv0 + 32 * hf + 8 * (col >> 2) + 4 * T + (col & 3), ktot - 1);
@@ -491,8 +509,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const int key = min(k0 + j, ktot - 1);
-                        const size_t at = KIND == PF_ROWS ? svb + (size_t)key * a.kvs + d : svb + (size_t)d * a.cap + key;
-                        x[j] = k0 + j < ktot ? vf32[at] : 0.0f;
+                        x[j] = k0 + j < ktot ? vf32[svb + (size_t)d * a.cap + key] : 0.0f;
                     }
                     sr[i][0] = make_float4(x[0], x[1], x[2], x[3]);
                     sr[i][1] = make_float4(x[4], x[5], x[6], x[7]);
@@ -501,10 +518,26 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
         }
     };
     auto stage_store = [&](half_t* dst) {
+        if constexpr (KIND == PF_ROWS) {
+            // Dim 4*rdq + e, keys 4*rkq .. +3: V fragment (half, t) = (rkq / 8,
+            // dim / 16), lane (dim % 16) + 16 * ((rkq % 8) / 2), halves 4 * (rkq % 2) ..
+            const float4 x[4] = {sr[KI][0], sr[KI][1], sr[KI + 1][0], sr[KI + 1][1]};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int dd = 4 * rdq + e;
+                half4 y;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) y[u] = to_h(e == 0 ? x[u].x : e == 1 ? x[u].y : e == 2 ? x[u].z : x[u].w);
+                const int frag = KF + (rkq >> 3) * NT + (dd >> 4);
+                const int ln = (dd & 15) + 16 * ((rkq & 7) >> 1);
+                *reinterpret_cast<half4*>(dst + frag * FH + ln * 8 + 4 * (rkq & 1)) = y;
+            }
+        }
         if constexpr (STAGED) {
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
                 const int f = wave + PW * i;
+                if (KIND == PF_ROWS && i >= KI) continue;
                 const float4 x0 = sr[i][0], x1 = sr[i][1];
                 half8 y;
                 y[0] = to_h(x0.x); y[1] = to_h(x0.y); y[2] = to_h(x0.z); y[3] = to_h(x0.w);

@@ -22,7 +22,8 @@ from . import _lib
 
 __all__ = [
     "CudaError", "UnsupportedAttention", "OddCacheCapacity", "CacheOverrun", "SliceOverrun", "RaggedBlock",
-    "MismatchedQ8", "OddHeadDim", "Driver", "NoDevice", "InvalidArgument", "DecodeScratch", "Q8", "KvCacheQ8",
+    "MismatchedQ8", "OddHeadDim", "Driver", "NoDevice", "InvalidArgument", "ScratchGrowthInCapture", "DecodeScratch",
+    "Q8", "KvCacheQ8",
     "TiledCache16", "Gpu",
 ]
 
@@ -77,8 +78,14 @@ class InvalidArgument(CudaError):
     status = 10
 
 
+class ScratchGrowthInCapture(CudaError):
+    """A decode scratch would have to grow while its stream captures a graph."""
+    status = 11
+
+
 _BY_STATUS = {c.status: c for c in (UnsupportedAttention, OddCacheCapacity, CacheOverrun, SliceOverrun,
-                                    RaggedBlock, MismatchedQ8, OddHeadDim, Driver, NoDevice, InvalidArgument)}
+                                    RaggedBlock, MismatchedQ8, OddHeadDim, Driver, NoDevice, InvalidArgument,
+                                    ScratchGrowthInCapture)}
 
 
 def _check(status: int):
