@@ -52,9 +52,11 @@ typedef enum llmtie_status {
     LLMTIE_DRIVER = 8,                /* Driver{what, source}             error.rs:281 */
     LLMTIE_NO_DEVICE = 9,             /* NoDevice(String)                 error.rs:242 */
     LLMTIE_INVALID_ARGUMENT = 10,     /* a null pointer where a buffer is required (no reference twin) */
-    LLMTIE_SCRATCH_GROWTH_IN_CAPTURE = 11 /* a decode scratch would have to grow while its stream captures a
-                                           * graph (no reference twin: the reference does not capture);
-                                           * fields: partial floats needed, held, counters needed, held */
+    LLMTIE_SCRATCH_GROWTH_IN_CAPTURE = 11, /* a decode scratch would have to grow while its stream captures a
+                                            * graph (no reference twin: the reference does not capture);
+                                            * fields: partial floats needed, held, counters needed, held */
+    LLMTIE_SCRATCH_LIMIT = 12              /* the fixed scratch of llmtie_attn_decode_f16_noalloc is too small
+                                            * for the call (no reference twin); fields as above */
 } llmtie_status;
 
 /* The last error raised on the calling thread: the status, up to four numeric
@@ -123,6 +125,19 @@ int llmtie_attn_decode_f16(void* stream, const float* q, size_t q_len, const uin
                            const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads, size_t head_dim,
                            size_t tk, size_t cap, float scale, int scale_q, llmtie_decode_scratch* scratch,
                            float* out, size_t out_len);
+
+/* No counterpart in the reference: llmtie_attn_decode_f16 for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and result bits, no
+ * scratch argument: the split partials and arrival counters live in a fixed
+ * 4.25 MiB device array the library holds on each device (1M partial floats,
+ * 256 kv heads' counters); a call that needs more is refused with
+ * LLMTIE_SCRATCH_LIMIT before any launch. It calls no allocator. Every call
+ * on one device shares that array, so calls that can overlap on one GPU (two
+ * streams, two threads) race and must not be made. */
+int llmtie_attn_decode_f16_noalloc(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
+                                   const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads, size_t head_dim,
+                                   size_t tk, size_t cap, float scale, int scale_q, float* out, size_t out_len);
 
 /* Gpu::attn_decode_f16_q (device.rs:5973): plus the context's int8 twin
  * (twin_len >= n + 4*(n/32) bytes, n = heads*head_dim). */

@@ -35,6 +35,7 @@ SIGNATURES = {
     "llmtie_flash_attn_f16": (I, [P, P, SZ, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, SZ, F, I]),
     "llmtie_flash_attn_rows": (I, [P, P, SZ, P, SZ, SZ, SZ, SZ, F]),
     "llmtie_attn_decode_f16": (I, [P, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ]),
+    "llmtie_attn_decode_f16_noalloc": (I, [P, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, SZ]),
     "llmtie_attn_decode_f16_q": (I, [P, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ, P, SZ]),
     "llmtie_attn_decode_f16_q_row": (I, [P, P, SZ, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, F, I, P, P, SZ, P, SZ,
                                          SZ, SZ]),

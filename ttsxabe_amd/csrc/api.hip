@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/llmtie_hip.h"
 #include "decode.h"
@@ -318,12 +319,21 @@ int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hi
     return LLMTIE_OK;
 }
 
+// Partials and counters of the no-allocation decode (device addresses).
+struct FixedScratch {
+    float* part;
+    size_t part_cap;  // floats
+    unsigned* ctr;
+    size_t ctr_cap;   // words
+};
+
 // The checks and the launch behind every single-sequence decode
 // (device.rs:6224-6410).
 int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q_off, const void* k, size_t k_len,
                   const void* v, size_t v_len, size_t heads, size_t kv_heads, size_t hd, size_t tk, size_t cap,
                   float scale, int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len,
-                  size_t out_off, int8_t* twin, size_t twin_rows, size_t twin_k, bool has_twin) {
+                  size_t out_off, int8_t* twin, size_t twin_rows, size_t twin_k, bool has_twin,
+                  const FixedScratch* fixed = nullptr) {
     const bool tiled = kind == KV_T16;
     if (!(hd == 64 || hd == 128)) return unsupported(hd, heads, kv_heads);
     if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 16) return unsupported(hd, heads, kv_heads);
@@ -351,15 +361,29 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
         if (!twin) return invalid("twin");
     }
     if (!q || !k || !v || !out) return invalid("a buffer");
-    if (!scratch) return invalid("scratch");
+    if (!scratch && !fixed) return invalid("scratch");
     const size_t group = heads / kv_heads;
     int nit, splits;
     plan_decode(tk, kv_heads, group, nit, splits);
     const size_t mls = ml_stride(splits, group);
     const size_t part = kv_heads * ((size_t)splits * group * hd + mls);
     const long ml_off = (long)(kv_heads * (size_t)splits * group * hd);
-    int r = ensure_scratch(scratch, part, kv_heads * CTR_STRIDE, S(stream));
-    if (r != LLMTIE_OK) return r;
+    float* part_p;
+    unsigned* ctr_p;
+    if (fixed) {
+        if (part > fixed->part_cap || kv_heads * CTR_STRIDE > fixed->ctr_cap)
+            return fail(LLMTIE_SCRATCH_LIMIT, part, fixed->part_cap, kv_heads * CTR_STRIDE, fixed->ctr_cap,
+                        "the call needs %zu partial floats and %zu counter words; the fixed scratch holds %zu and "
+                        "%zu",
+                        part, kv_heads * CTR_STRIDE, fixed->part_cap, fixed->ctr_cap);
+        part_p = fixed->part;
+        ctr_p = fixed->ctr;
+    } else {
+        int r = ensure_scratch(scratch, part, kv_heads * CTR_STRIDE, S(stream));
+        if (r != LLMTIE_OK) return r;
+        part_p = scratch->part;
+        ctr_p = scratch->ctr;
+    }
     DecodeArgs a;
     memset(&a, 0, sizeof a);
     a.q = q;
@@ -370,9 +394,9 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
         a.twin_codes = twin;
         a.twin_scales = reinterpret_cast<float*>(twin + twin_rows * twin_k);
     }
-    a.part = scratch->part;
+    a.part = part_p;
     a.ml_off = ml_off;
-    a.ctr = scratch->ctr;
+    a.ctr = ctr_p;
     a.q_off = (long)q_off;
     a.out_off = (long)out_off;
     a.tk = (int)tk;
@@ -448,6 +472,63 @@ int llmtie_attn_decode_f16(void* stream, const float* q, size_t q_len, const uin
                            float* out, size_t out_len) {
     return decode_common(stream, KV_F16, q, q_len, 0, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap, scale,
                          scale_q, scratch, out, out_len, 0, nullptr, 0, 0, false);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------ decode without allocation
+//
+// `scratch`: the split partials (NOALLOC_PART_FLOATS floats) then the arrival
+// counters (NOALLOC_CTR_WORDS words, CTR_STRIDE per kv head) of
+// llmtie_attn_decode_f16_noalloc, 4.25 MiB held on every device the library
+// runs on until the process ends. Host code never passes the array's name
+// (a host-side stand-in, not a device address) to the device: it uses the
+// address hipGetSymbolAddress gives for the current device, obtained once per
+// device.
+constexpr size_t NOALLOC_PART_FLOATS = (size_t)1 << 20;
+constexpr size_t NOALLOC_CTR_WORDS = (size_t)256 * CTR_STRIDE;
+static __device__ __align__(256) float scratch[NOALLOC_PART_FLOATS + NOALLOC_CTR_WORDS];
+
+namespace {
+
+std::mutex noalloc_mu;
+float* noalloc_ptr[64];
+
+// This device's copy of `scratch`, its counters cleared on first use (by a
+// kernel on `st`; every call leaves them at zero afterwards).
+int noalloc_scratch(hipStream_t st, FixedScratch& f) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return driver("hipGetDevice", e);
+    if (dev < 0 || dev >= 64) return driver("device index", hipErrorInvalidDevice);
+    std::lock_guard<std::mutex> lock(noalloc_mu);
+    if (!noalloc_ptr[dev]) {
+        float* p = nullptr;
+        e = hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return driver("hipGetSymbolAddress(scratch)", e);
+        e = launch_fill_u32(reinterpret_cast<unsigned*>(p + NOALLOC_PART_FLOATS), NOALLOC_CTR_WORDS, 0u, st);
+        if (e != hipSuccess) return driver("clearing the fixed scratch", e);
+        noalloc_ptr[dev] = p;
+    }
+    f.part = noalloc_ptr[dev];
+    f.part_cap = NOALLOC_PART_FLOATS;
+    f.ctr = reinterpret_cast<unsigned*>(noalloc_ptr[dev] + NOALLOC_PART_FLOATS);
+    f.ctr_cap = NOALLOC_CTR_WORDS;
+    return LLMTIE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmtie_attn_decode_f16_noalloc(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
+                                   const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads, size_t head_dim,
+                                   size_t tk, size_t cap, float scale, int scale_q, float* out, size_t out_len) {
+    FixedScratch f;
+    int r = noalloc_scratch(S(stream), f);
+    if (r != LLMTIE_OK) return r;
+    return decode_common(stream, KV_F16, q, q_len, 0, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap, scale,
+                         scale_q, nullptr, out, out_len, 0, nullptr, 0, 0, false, &f);
 }
 
 int llmtie_attn_decode_f16_q(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,

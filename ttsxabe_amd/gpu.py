@@ -22,7 +22,8 @@ from . import _lib
 
 __all__ = [
     "CudaError", "UnsupportedAttention", "OddCacheCapacity", "CacheOverrun", "SliceOverrun", "RaggedBlock",
-    "MismatchedQ8", "OddHeadDim", "Driver", "NoDevice", "InvalidArgument", "ScratchGrowthInCapture", "DecodeScratch",
+    "MismatchedQ8", "OddHeadDim", "Driver", "NoDevice", "InvalidArgument", "ScratchGrowthInCapture", "ScratchLimit",
+    "DecodeScratch",
     "Q8", "KvCacheQ8",
     "TiledCache16", "Gpu",
 ]
@@ -83,9 +84,14 @@ class ScratchGrowthInCapture(CudaError):
     status = 11
 
 
+class ScratchLimit(CudaError):
+    """The fixed scratch of attn_decode_f16_noalloc is too small for the call."""
+    status = 12
+
+
 _BY_STATUS = {c.status: c for c in (UnsupportedAttention, OddCacheCapacity, CacheOverrun, SliceOverrun,
                                     RaggedBlock, MismatchedQ8, OddHeadDim, Driver, NoDevice, InvalidArgument,
-                                    ScratchGrowthInCapture)}
+                                    ScratchGrowthInCapture, ScratchLimit)}
 
 
 def _check(status: int):
@@ -255,6 +261,22 @@ class Gpu:
         _check(self._L.llmtie_attn_decode_f16(self._stream(), _p(q), _n(q), _p(k), _n(k), _p(v), _n(v), heads,
                                               kv_heads, head_dim, tk, cap, C.c_float(scale), int(bool(scale_q)),
                                               scratch.handle, _p(out), n))
+        return out
+
+    def attn_decode_f16_noalloc(self, q, k, v, heads, kv_heads, head_dim, tk, cap, scale, scale_q, out=None):
+        """attn_decode_f16 without a scratch: the library's fixed per-device
+        scratch (no reference counterpart; for callers that cannot allocate).
+        Calls that can overlap on one device race."""
+        _need(q, _F32, "q")
+        _need(k, _H16, "k")
+        _need(v, _H16, "v")
+        _need(out, _F32, "out")
+        n = heads * head_dim
+        if out is None:
+            out = torch.empty(n, dtype=torch.float32, device=self.device)
+        _check(self._L.llmtie_attn_decode_f16_noalloc(self._stream(), _p(q), _n(q), _p(k), _n(k), _p(v), _n(v),
+                                                      heads, kv_heads, head_dim, tk, cap, C.c_float(scale),
+                                                      int(bool(scale_q)), _p(out), _n(out)))
         return out
 
     def q8_zeros(self, rows: int, k: int) -> Q8:
