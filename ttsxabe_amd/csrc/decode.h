@@ -59,6 +59,10 @@ struct DecodeArgs {
     // if not, the head's context is written as NaN, never silently wrong.
     int xcd;
     int xcd_fake;  // tests only: report XCC id (L / 8) % 8 instead of the real one
+    // Workgroups of the launch / 8, set by launch_decode: the kernel reads it
+    // with its other arguments rather than from the dispatch packet (a second
+    // scalar-memory round trip before the first K/V load).
+    int grid8;
 };
 
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);

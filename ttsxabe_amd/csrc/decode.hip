@@ -588,7 +588,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     int split = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
     const int nit = a.nit;
     if (a.xcd) {
-        const int item = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+        const int item = (int)(blockIdx.x % 8) * a.grid8 + (int)(blockIdx.x / 8);
         split = item % a.splits;
         h = (item / a.splits) % a.kv_heads;
         seq = item / (a.splits * a.kv_heads);
@@ -1101,7 +1101,7 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
 
     const SkSeqs sq = sk_seqs(a, lane);
     const long total = sq.total;
-    const long nw = min((long)gridDim.x * DW, total);
+    const long nw = min((long)a.items * DW, total);
     const long u = (long)blockIdx.x * DW + wave;
 
     // A sequence the batch describes wrongly gets a NaN row (written by the
@@ -1504,11 +1504,13 @@ static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_head
     }
     const dim3 grid = a.xcd ? dim3(a.splits * kv_heads * nseq) : dim3(a.splits, kv_heads, nseq);
     dim3 block(DT);
+    DecodeArgs b = a;
+    b.grid8 = (int)(grid.x / 8);
     const int esz = kind == KV_F32 ? 4 : 2;
     const int va = (kind == KV_T16 || kind == KV_TQ8) ? 16 : (((long)a.cap * esz) % 16 == 0 ? 16 : 8);
 #define L(HD, KIND, VA)                                                                        \
     if (hd == HD && kind == KIND && va == VA) {                                                \
-        hipLaunchKernelGGL((attn_decode_kernel<HD, KIND, VA>), grid, block, 0, st, a);          \
+        hipLaunchKernelGGL((attn_decode_kernel<HD, KIND, VA>), grid, block, 0, st, b);          \
         return hipGetLastError();                                                              \
     }
     L(64, KV_F16, 16) L(128, KV_F16, 16) L(64, KV_F16, 8) L(128, KV_F16, 8)

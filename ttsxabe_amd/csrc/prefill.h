@@ -35,6 +35,7 @@ struct PrefillArgs {
     // of whole groups and read their K/V through their own L2 (C3 at 8192
     // rows: 767 -> 679 us).
     int xcd, nrb;
+    int grid8;  // workgroups of the 1-D launch / 8 (read with the arguments, not from the dispatch packet)
 };
 
 // nqt: 16-query tiles per wave (1, 2 or 4).

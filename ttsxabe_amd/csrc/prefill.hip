@@ -429,7 +429,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     const int group = a.heads / a.kv_heads;
     int rb = blockIdx.x, gy = blockIdx.y;
     if (a.xcd) {
-        const int item = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+        const int item = (int)(blockIdx.x % 8) * a.grid8 + (int)(blockIdx.x / 8);
         gy = item / a.nrb;
         rb = item % a.nrb;
     }
@@ -836,6 +836,7 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
         b.nrb = (int)grid.x;
         const unsigned items = grid.x * grid.y;
         b.xcd = items % 8 == 0 && !(getenv("LLMTIE_PREFILL_XCD") && !atoi(getenv("LLMTIE_PREFILL_XCD")));
+        b.grid8 = (int)(items / 8);
         const dim3 g = b.xcd ? dim3(items) : grid;
 #define F(HD, KIND, NQ)                                                                    \
     if (hd == HD && kind == KIND && nqt == NQ) {                                           \
