@@ -556,6 +556,150 @@ __device__ __forceinline__ void merge_head(const float* po, const float* pml, in
 }
 
 
+// ------------------------------------------------------------------------
+// Group-1 (MHA) decode on the VALU. With one query head per kv head an MFMA
+// tile would carry one live column of 16, and an f32 operand would need hi +
+// lo f16 halves; here every product is an f32 FMA (f16 cache values convert
+// exactly), as in the reference's own f32 arithmetic.
+//
+// The block's K and V arrive in the same fragment order as for the MFMA path
+// (lane (col, grp) holds key 8*(col/4) + 4T + col%4, dims 32s + 8grp .. +7 of
+// K, and dim 16t + col, keys 8grp .. +7 of V): a lane's partial dot products
+// over its 8 * HD/32 dims are summed over the four lanes of its column
+// (sum4grp), the block's probabilities go through a 32-float LDS row so each
+// lane can read the eight it needs for V, and a lane's context sums for dims
+// 16t + col are summed over the four grp lanes once, after the last block.
+
+// f32 cache values for the VALU fold (no hi/lo split).
+template <int HD>
+struct FragF32 {
+    float4 k[2][HD / 32][2];
+    float4 v[HD / 16][2];
+};
+
+// The 32-key block at p0 of an f32 reference-layout cache, raw. FULL: every
+// key of the block is live; else keys >= tk read as zero.
+template <int HD, int VA, bool FULL>
+__device__ __forceinline__ void load_block_f32v(const Ctx& c, int p0, int lane, FragF32<HD>& f) {
+    constexpr int NS = HD / 32, NT = HD / 16;
+    const int col = lane & 15, grp = lane >> 4;
+    const float* kb = reinterpret_cast<const float*>(c.k);
+    const float* vb = reinterpret_cast<const float*>(c.v);
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+        const int key = p0 + 8 * (col >> 2) + 4 * T + (col & 3);
+        const bool ok = FULL || key < c.tk;
+        const int kk = ok ? key : 0;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const float4* p = reinterpret_cast<const float4*>(kb + (size_t)kk * HD + 32 * s + 8 * grp);
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 x0 = p[0], x1 = p[1];
+            f.k[T][s][0] = ok ? x0 : z;
+            f.k[T][s][1] = ok ? x1 : z;
+        }
+    }
+    const int k0 = p0 + 8 * grp;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float* r = vb + (size_t)(16 * t + col) * c.cap + k0;
+        if constexpr (FULL && VA == 16) {
+            f.v[t][0] = reinterpret_cast<const float4*>(r)[0];
+            f.v[t][1] = reinterpret_cast<const float4*>(r)[1];
+        } else if constexpr (FULL) {
+            const float2 a0 = reinterpret_cast<const float2*>(r)[0], a1 = reinterpret_cast<const float2*>(r)[1];
+            const float2 a2 = reinterpret_cast<const float2*>(r)[2], a3 = reinterpret_cast<const float2*>(r)[3];
+            f.v[t][0] = make_float4(a0.x, a0.y, a1.x, a1.y);
+            f.v[t][1] = make_float4(a2.x, a2.y, a3.x, a3.y);
+        } else {
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = k0 + j < c.tk ? r[j] : 0.0f;
+            f.v[t][0] = make_float4(x[0], x[1], x[2], x[3]);
+            f.v[t][1] = make_float4(x[4], x[5], x[6], x[7]);
+        }
+    }
+}
+
+// Element j of a lane's 8-element K or V run, as f32.
+template <int HD, int KIND, typename FR>
+__device__ __forceinline__ float g1_k(const FR& f, int T, int s, int j) {
+    if constexpr (KIND == KV_F32) {
+        const float4& x = f.k[T][s][j >> 2];
+        return (j & 3) == 0 ? x.x : (j & 3) == 1 ? x.y : (j & 3) == 2 ? x.z : x.w;
+    } else {
+        return (float)f.k[T][s][j];
+    }
+}
+template <int HD, int KIND, typename FR>
+__device__ __forceinline__ float g1_v(const FR& f, int t, int j) {
+    if constexpr (KIND == KV_F32) {
+        const float4& x = f.v[t][j >> 2];
+        return (j & 3) == 0 ? x.x : (j & 3) == 1 ? x.y : (j & 3) == 2 ? x.z : x.w;
+    } else {
+        return (float)f.v[t][j];
+    }
+}
+
+// One 32-key block folded into the wave's running (m, l, o) for its one
+// query: qv holds the lane's query dims 32s + 8grp + j, already in log2-score
+// units; o[t] is this lane's context sum for dim 16t + col over keys 8grp ..
+// of every block; m and l are wave-uniform. pw: the wave's 32-float LDS row.
+template <int HD, int KIND, bool MASK, typename FR>
+__device__ __forceinline__ void fold_block_g1(const FR& f, const float (&qv)[HD / 32][8], int p0, int tk, int col,
+                                              int grp, float& m_run, float& l_run, float (&o)[HD / 16],
+                                              float* pw) {
+    constexpr int NS = HD / 32, NT = HD / 16;
+    float sc[2];
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(g1_k<HD, KIND>(f, T, s, j), qv[s][j], acc);
+        acc = sum4grp(acc);
+        if constexpr (MASK) {
+            const int key = p0 + 8 * (col >> 2) + 4 * T + (col & 3);
+            acc = key < tk ? acc : ninf();
+        }
+        sc[T] = acc;
+    }
+    const float mx = wave_max(fmaxf(sc[0], sc[1]));
+    const float mn = fmaxf(m_run, mx);
+    const float fac = ex2(m_run - mn);
+    m_run = mn;
+    const float e0 = ex2(sc[0] - mn), e1 = ex2(sc[1] - mn);
+    // Each key's probability sits in the four grp lanes of its column: the
+    // wave sum is four times the block's (an exact scaling).
+    l_run = l_run * fac + wave_sum(e0 + e1) * 0.25f;
+    if (__any(fac != 1.0f)) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) o[t] *= fac;
+    }
+    if (grp == 0) {
+        pw[8 * (col >> 2) + (col & 3)] = e0;
+        pw[8 * (col >> 2) + 4 + (col & 3)] = e1;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float4 pa = *reinterpret_cast<const float4*>(pw + 8 * grp);
+    const float4 pb = *reinterpret_cast<const float4*>(pw + 8 * grp + 4);
+    const float pp[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float acc = o[t];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = g1_v<HD, KIND>(f, t, j);
+            // A tiled cache may hold non-finite garbage past tk: 0 * NaN is NaN.
+            if constexpr (MASK && KIND == KV_T16) v = p0 + 8 * grp + j < tk ? v : 0.0f;
+            acc = __builtin_fmaf(pp[j], v, acc);
+        }
+        o[t] = acc;
+    }
+    __builtin_amdgcn_wave_barrier();  // the row is read before the next block's writes
+}
+
 // The hardware id of the XCD this wave runs on (HW_REG_XCC_ID, bits 3:0).
 __device__ __forceinline__ unsigned xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15u; }
 
@@ -572,7 +716,7 @@ __device__ __forceinline__ bool one_xcd(unsigned long long c) {
     return n * s2 == s1 * s1;
 }
 
-template <int HD, int KIND, int VA>
+template <int HD, int KIND, int VA, bool G1>
 __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel(DecodeArgs a) {
     constexpr int NS = HD / 32;
     constexpr int NT = HD / 16;
@@ -581,6 +725,9 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     __shared__ float lds[DW * OBW];
     __shared__ float wm[DW][16], wl[DW][16], gl[16];
     __shared__ int last;
+    __shared__ __attribute__((aligned(16))) float prow[DW][32];  // G1: a block's probabilities
+    static_assert(!G1 || KIND != KV_TQ8, "the Q8_0 cache decodes through the MFMA path");
+    using FR = std::conditional_t<G1 && KIND == KV_F32, FragF32<HD>, Frag<HD, KIND>>;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -631,12 +778,17 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const int nfull = tk >> 5;
     const int nf = nfull > first ? min(nit, (nfull - first + DW - 1) / DW) : 0;
     const bool tail = (tk & 31) && nfull >= first && (nfull - first) % DW == 0 && (nfull - first) / DW < nit;
-    Frag<HD, KIND> f0, f1;
+    FR f0, f1;
+    auto ld = [&](int p, FR& f, auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        if constexpr (G1 && KIND == KV_F32) load_block_f32v<HD, VA, FULL>(c, p, lane, f);
+        else load_block<HD, KIND, VA, FULL>(c, p, lane, f);
+    };
     // The first two blocks go out before the queries are read: the queries'
     // first use waits for every load issued before them, so a block issued
     // after that would start a second memory round trip.
-    if (nf > 0) load_block<HD, KIND, VA, true>(c, first * 32, lane, f0);
-    if (nf > 1) load_block<HD, KIND, VA, true>(c, (first + DW) * 32, lane, f1);
+    if (nf > 0) ld(first * 32, f0, std::true_type{});
+    if (nf > 1) ld((first + DW) * 32, f1, std::true_type{});
 
     // The group's queries as B operands, hi + lo (columns past the group are
     // read from column 0 and zeroed, so every load is unconditional). The
@@ -652,23 +804,39 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         qx[s][1] = reinterpret_cast<const float4*>(qc + 32 * s)[1];
     }
     half8 qh[NS], ql[NS];
+    float qv[NS][8];  // G1: the query in f32, log2-score units
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         const float x[8] = {qx[s][0].x, qx[s][0].y, qx[s][0].z, qx[s][0].w,
                             qx[s][1].x, qx[s][1].y, qx[s][1].z, qx[s][1].w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            half_t hh, ll;
-            split_h(qok ? x[j] * a.qscale * a.score_l2 : 0.0f, hh, ll);
-            qh[s][j] = hh;
-            ql[s][j] = ll;
+            if constexpr (G1) {
+                qv[s][j] = x[j] * a.qscale * a.score_l2;
+            } else {
+                half_t hh, ll;
+                split_h(qok ? x[j] * a.qscale * a.score_l2 : 0.0f, hh, ll);
+                qh[s][j] = hh;
+                ql[s][j] = ll;
+            }
         }
     }
 
     float m_run = ninf(), l_run = 0.0f;
     floatx4 o[NT];
+    float o1[NT];  // G1: lane's context sums for dims 16t + col
 #pragma unroll
-    for (int t = 0; t < NT; ++t) o[t] = zero_f4();
+    for (int t = 0; t < NT; ++t) {
+        o[t] = zero_f4();
+        o1[t] = 0.0f;
+    }
+    auto fold = [&](const FR& f, int p, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        if constexpr (G1)
+            fold_block_g1<HD, KIND, MASK>(f, qv, p, tk, col, grp, m_run, l_run, o1, prow[wave]);
+        else
+            fold_block<HD, KIND, MASK>(f, qh, ql, p, tk, grp, a.score_l2, m_run, l_run, o);
+    };
 
     // Two blocks in flight: while block i is folded, block i + 1 is on its
     // way. Inside the loop every prefetch is unconditional (a block past this
@@ -684,25 +852,29 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         const int p1 = (first + (i + 1) * DW) * 32;
         const int p2 = (first + (i + 2) * DW) * 32;
         const int p3 = (first + min(i + 3, nf - 1) * DW) * 32;
-        fold_block<HD, KIND, false>(f0, qh, ql, p0, tk, grp, a.score_l2, m_run, l_run, o);
+        fold(f0, p0, std::false_type{});
         __builtin_amdgcn_sched_barrier(0);
-        load_block<HD, KIND, VA, true>(c, p2, lane, f0);
+        ld(p2, f0, std::true_type{});
         __builtin_amdgcn_sched_barrier(0);
-        fold_block<HD, KIND, false>(f1, qh, ql, p1, tk, grp, a.score_l2, m_run, l_run, o);
+        fold(f1, p1, std::false_type{});
         __builtin_amdgcn_sched_barrier(0);
-        load_block<HD, KIND, VA, true>(c, p3, lane, f1);
+        ld(p3, f1, std::true_type{});
         __builtin_amdgcn_sched_barrier(0);
     }
     // The last one or two blocks (already in f0, f1).
-    if (i < nf) fold_block<HD, KIND, false>(f0, qh, ql, (first + i * DW) * 32, tk, grp, a.score_l2, m_run, l_run, o);
-    if (i + 1 < nf)
-        fold_block<HD, KIND, false>(f1, qh, ql, (first + (i + 1) * DW) * 32, tk, grp, a.score_l2, m_run, l_run,
-                                    o);
+    if (i < nf) fold(f0, (first + i * DW) * 32, std::false_type{});
+    if (i + 1 < nf) fold(f1, (first + (i + 1) * DW) * 32, std::false_type{});
     if (tail) {
-        load_block<HD, KIND, VA, TILED>(c, nfull * 32, lane, f0);
-        fold_block<HD, KIND, true>(f0, qh, ql, nfull * 32, tk, grp, a.score_l2, m_run, l_run, o);
+        ld(nfull * 32, f0, std::integral_constant<bool, TILED>{});
+        fold(f0, nfull * 32, std::true_type{});
     }
-    l_run = sum4grp(l_run);
+    if constexpr (G1) {
+        // A wave with no block keeps m = -inf, l = 0, o = 0 (weight 0 below).
+#pragma unroll
+        for (int t = 0; t < NT; ++t) o1[t] = sum4grp(o1[t]);
+    } else {
+        l_run = sum4grp(l_run);
+    }
 
     // Combine the four waves: each wave leaves its (m, l) and its unscaled
     // O^T in LDS ([query column][dim], 16-byte writes), one barrier, and the
@@ -712,9 +884,16 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         wl[wave][col] = l_run;
     }
     float* ob = lds + wave * OBW;
+    if constexpr (G1) {
+        if (grp == 0) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-        *reinterpret_cast<floatx4*>(&ob[col * (HD + 4) + 16 * t + 4 * grp]) = o[t];
+            for (int t = 0; t < NT; ++t) ob[16 * t + col] = o1[t];
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            *reinterpret_cast<floatx4*>(&ob[col * (HD + 4) + 16 * t + 4 * grp]) = o[t];
+    }
     __syncthreads();
     // Wave weights of query column g, and its combined normaliser.
     auto weights = [&](int g, float (&f)[DW]) {
@@ -1474,10 +1653,12 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     }
 }
 
-#define DECODE_INST(HD, KIND, VA) template __global__ void attn_decode_kernel<HD, KIND, VA>(DecodeArgs);
-DECODE_INST(64, KV_F16, 16) DECODE_INST(128, KV_F16, 16) DECODE_INST(64, KV_F16, 8) DECODE_INST(128, KV_F16, 8)
-DECODE_INST(64, KV_F32, 16) DECODE_INST(128, KV_F32, 16) DECODE_INST(64, KV_F32, 8) DECODE_INST(128, KV_F32, 8)
-DECODE_INST(64, KV_T16, 16) DECODE_INST(128, KV_T16, 16) DECODE_INST(64, KV_TQ8, 16) DECODE_INST(128, KV_TQ8, 16)
+#define DECODE_INST(HD, KIND, VA, G1) template __global__ void attn_decode_kernel<HD, KIND, VA, G1>(DecodeArgs);
+#define DECODE_INST2(HD, KIND, VA) DECODE_INST(HD, KIND, VA, false) DECODE_INST(HD, KIND, VA, true)
+DECODE_INST2(64, KV_F16, 16) DECODE_INST2(128, KV_F16, 16) DECODE_INST2(64, KV_F16, 8) DECODE_INST2(128, KV_F16, 8)
+DECODE_INST2(64, KV_F32, 16) DECODE_INST(128, KV_F32, 16, false) DECODE_INST2(64, KV_F32, 8)
+DECODE_INST(128, KV_F32, 8, false) DECODE_INST2(64, KV_T16, 16) DECODE_INST2(128, KV_T16, 16)
+DECODE_INST(64, KV_TQ8, 16, false) DECODE_INST(128, KV_TQ8, 16, false)
 
 template __global__ void attn_decode_sk_kernel<64>(DecodeArgs);
 template __global__ void attn_decode_sk_kernel<128>(DecodeArgs);
@@ -1508,14 +1689,20 @@ static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_head
     b.grid8 = (int)(grid.x / 8);
     const int esz = kind == KV_F32 ? 4 : 2;
     const int va = (kind == KV_T16 || kind == KV_TQ8) ? 16 : (((long)a.cap * esz) % 16 == 0 ? 16 : 8);
-#define L(HD, KIND, VA)                                                                        \
-    if (hd == HD && kind == KIND && va == VA) {                                                \
-        hipLaunchKernelGGL((attn_decode_kernel<HD, KIND, VA>), grid, block, 0, st, b);          \
+    // Group 1 (MHA) folds on the VALU, except f32 caches at head_dim 128
+    // (their raw blocks would not fit two deep in registers).
+    const bool g1 = a.group == 1 && kind != KV_TQ8 && !(kind == KV_F32 && hd == 128) &&
+                    !getenv("LLMTIE_DECODE_G1_MFMA");
+#define L(HD, KIND, VA, G1)                                                                    \
+    if (hd == HD && kind == KIND && va == VA && g1 == G1) {                                    \
+        hipLaunchKernelGGL((attn_decode_kernel<HD, KIND, VA, G1>), grid, block, 0, st, b);      \
         return hipGetLastError();                                                              \
     }
-    L(64, KV_F16, 16) L(128, KV_F16, 16) L(64, KV_F16, 8) L(128, KV_F16, 8)
-    L(64, KV_F32, 16) L(128, KV_F32, 16) L(64, KV_F32, 8) L(128, KV_F32, 8)
-    L(64, KV_T16, 16) L(128, KV_T16, 16) L(64, KV_TQ8, 16) L(128, KV_TQ8, 16)
+#define L2(HD, KIND, VA) L(HD, KIND, VA, false) L(HD, KIND, VA, true)
+    L2(64, KV_F16, 16) L2(128, KV_F16, 16) L2(64, KV_F16, 8) L2(128, KV_F16, 8)
+    L2(64, KV_F32, 16) L(128, KV_F32, 16, false) L2(64, KV_F32, 8) L(128, KV_F32, 8, false)
+    L2(64, KV_T16, 16) L2(128, KV_T16, 16) L(64, KV_TQ8, 16, false) L(128, KV_TQ8, 16, false)
+#undef L2
 #undef L
     return hipErrorInvalidValue;
 }
