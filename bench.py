@@ -46,7 +46,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", metavar="NAME",
                     help="run one secondary workload (c3_prefill_8192_steady, c3_prefill_512, c4_encoder, "
-                         "c5_q8_batch_decode, practical_peaks) and print its line alone, for profiling runs")
+                         "c5_q8_batch_decode, practical_peaks, reference_rows) and print its line alone, for "
+                         "profiling runs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB a few times (the known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -236,6 +237,57 @@ def bench_q8_batch(torch, g, steps, warmup):
                 frac=gbs / HBM_PEAK_GBS, tokens_per_s=nseq / (us * 1e-6))
 
 
+# The reference's own published rows for this path (one Quadro RTX 8000;
+# docs/KERNELS.md:1396-1403, :1253-1256, docs/BENCHMARKS.md:2197-2199), as
+# (name, kind, shape, published ms). Decode rows are ms per 32 layers of one
+# step; prefill rows are ms per layer.
+REFERENCE_ROWS = [
+    ("chat 8B decode, 128 ctx", "decode", dict(heads=32, kv=8, hd=128, tk=128), 0.42),
+    ("chat 8B decode, 512 ctx", "decode", dict(heads=32, kv=8, hd=128, tk=512), 0.45),
+    ("chat 8B decode, 1024 ctx", "decode", dict(heads=32, kv=8, hd=128, tk=1024), 0.60),
+    ("chat 8B decode, 2048 ctx", "decode", dict(heads=32, kv=8, hd=128, tk=2048), 1.17),
+    ("chat 8B decode, 4096 ctx", "decode", dict(heads=32, kv=8, hd=128, tk=4096), 1.522),
+    ("chat 8B decode, 8192 ctx", "decode", dict(heads=32, kv=8, hd=128, tk=8192), 2.548),
+    ("translator 13B decode, 128 ctx", "decode", dict(heads=40, kv=40, hd=128, tk=128), 0.44),
+    ("translator 13B decode, 1024 ctx", "decode", dict(heads=40, kv=40, hd=128, tk=1024), 1.61),
+    ("translator 13B decode, 4000 ctx", "decode", dict(heads=40, kv=40, hd=128, tk=4000), 5.390),
+    ("Whisper self decode, 40 of 448 (f32 cache)", "decode", dict(heads=20, kv=20, hd=64, tk=40, cap=448, f32=True,
+                                                                  scale_q=True), 0.18),
+    ("Whisper cross decode, 1500", "decode", dict(heads=20, kv=20, hd=64, tk=1500, scale_q=True), 0.76),
+    ("chat 8B prefill, 2048 positions", "prefill", dict(heads=32, kv=8, hd=128, tq=2048), 0.95),
+    ("chat 8B prefill, 8192 positions", "prefill", dict(heads=32, kv=8, hd=128, tq=8192), 11.0),
+    ("translator 13B prefill, 3968 positions", "prefill", dict(heads=40, kv=40, hd=128, tq=3968), 3.25),
+    ("Whisper encoder, 1500 frames", "encoder", dict(t=1500, heads=20, hd=64), 0.43),
+]
+
+
+def bench_reference_rows(torch, g, steps, warmup):
+    """Each published row of the reference at its own shape, through the
+    drop-in entry points on the reference's own layouts (f16 K [kv][cap][hd],
+    V [kv][hd][cap]; the f32 cache where it keeps one), timed as the other
+    lines are (HIP-graph replays over caches rotated past the LLC)."""
+    out = {}
+    for name, kind, c, ref_ms in REFERENCE_ROWS:
+        if kind == "decode":
+            r = bench_decode_f16(torch, g, c["heads"], c["kv"], c["hd"], c["tk"], c.get("cap", c["tk"]),
+                                 c.get("scale_q", False), steps, warmup, 32, f32_cache=c.get("f32", False))
+            ms = r["us_per_launch"] * 32 / 1e3
+            row = dict(ms_32_layers=round(ms, 4), gbs=round(r["gbs"], 1), frac=round(r["frac"], 4))
+        elif kind == "prefill":
+            r = bench_prefill(torch, g, c["tq"], c["heads"], c["kv"], c["hd"], max(3, steps // 4), 2,
+                              4 if c["tq"] >= 4096 else 32, tiled=False)
+            ms = r["us_per_launch"] / 1e3
+            row = dict(ms_per_layer=round(ms, 4), tflops=round(r["tflops"], 1), frac=round(r["frac"], 4))
+        else:
+            r = bench_encoder(torch, g, c["t"], c["heads"], c["hd"], steps, warmup, 32)
+            ms = r["us_per_launch"] / 1e3
+            row = dict(ms_per_layer=round(ms, 4), tflops=round(r["tflops"], 1), frac=round(r["frac"], 4))
+        row["reference_rtx8000_ms"] = ref_ms
+        row["speedup_vs_reference"] = round(ref_ms / ms, 2)
+        out[name] = row
+    return out
+
+
 def practical_peaks(torch):
     """What this box sustains outside the hot path, measured in the same run
     as context for the spec peaks the fractions use: an 8192^3 f16 GEMM
@@ -372,6 +424,7 @@ def main():
             "c4_encoder": lambda: bench_encoder(torch, g, 1500, 20, 64, a.steps, a.warmup, a.layers),
             "c5_q8_batch_decode": lambda: bench_q8_batch(torch, g, a.steps, a.warmup),
             "practical_peaks": lambda: practical_peaks(torch),
+            "reference_rows": lambda: bench_reference_rows(torch, g, a.steps, a.warmup),
         }
         if a.only not in only:
             print(json.dumps({"error": f"--only takes one of {sorted(only)}"}))
@@ -431,6 +484,8 @@ def main():
             for k2 in list(v):
                 if isinstance(v[k2], float):
                     v[k2] = round(v[k2], 4)
+        print("bench: the reference's published shapes", file=sys.stderr, flush=True)
+        sec["reference_rows"] = bench_reference_rows(torch, g, steps, a.warmup)
         # The peak the secondary numbers are fractions of, for reading them,
         # and what the box sustains outside the hot path.
         sec["peaks"] = {"hbm_gbs": HBM_PEAK_GBS, "f16_mfma_tflops": F16_PEAK_TFLOPS}
