@@ -45,9 +45,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", metavar="NAME",
-                    help="run one secondary workload (c3_prefill_8192_steady, c3_prefill_512, c4_encoder, "
-                         "c5_q8_batch_decode, practical_peaks, reference_rows) and print its line alone, for "
-                         "profiling runs")
+                    help="run one workload alone and print its line, for profiling runs: c2_decode, "
+                         "c3_prefill_512, c3_prefill_128, c3_prefill_8192_steady, c4_encoder, c4_cross_decode, "
+                         "c4_self_decode_224_f32, c5_q8_batch_decode, practical_peaks, reference_rows")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB a few times (the known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -419,6 +419,13 @@ def main():
     g = Gpu(0)
     if a.only:
         only = {
+            "c2_decode": lambda: bench_decode_f16(torch, g, 32, 8, 128, 4096, 4096, False, a.steps, a.warmup,
+                                                  a.layers, tiled=True),
+            "c4_cross_decode": lambda: bench_decode_f16(torch, g, 20, 20, 64, 1500, 1500, True, a.steps, a.warmup,
+                                                        a.layers, tiled=True),
+            "c4_self_decode_224_f32": lambda: bench_decode_f16(torch, g, 20, 20, 64, 224, 448, True, a.steps,
+                                                               a.warmup, a.layers, f32_cache=True),
+            "c3_prefill_128": lambda: bench_prefill(torch, g, 128, 32, 8, 128, a.steps, a.warmup, a.layers),
             "c3_prefill_8192_steady": lambda: bench_prefill(torch, g, 8192, 32, 8, 128, 5, 2, 4),
             "c3_prefill_512": lambda: bench_prefill(torch, g, 512, 32, 8, 128, a.steps, a.warmup, a.layers),
             "c4_encoder": lambda: bench_encoder(torch, g, 1500, 20, 64, a.steps, a.warmup, a.layers),

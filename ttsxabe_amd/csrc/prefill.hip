@@ -529,7 +529,11 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) y[u] = to_h(e == 0 ? x[u].x : e == 1 ? x[u].y : e == 2 ? x[u].z : x[u].w);
                 const int frag = KF + (rkq >> 3) * NT + (dd >> 4);
-                const int ln = (dd & 15) + 16 * ((rkq & 7) >> 1);
+                // Chunk (lane) index XOR the dim tile: a wave's 16 dims of one
+                // instruction land on 16 distinct 16-byte bank slots (unswizzled,
+                // the four dim tiles' chunks share 4 slots). The fragment read
+                // applies the same XOR (rows_lane).
+                const int ln = ((dd & 15) + 16 * ((rkq & 7) >> 1)) ^ (dd >> 4);
                 *reinterpret_cast<half4*>(dst + frag * FH + ln * 8 + 4 * (rkq & 1)) = y;
             }
         }
@@ -713,7 +717,8 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const half8 af = vf[(hf * NT + t) * 64 + lane];
+                // Rows: V chunks are swizzled by the dim tile (stage_store).
+                const half8 af = vf[(hf * NT + t) * 64 + (KIND == PF_ROWS ? (lane ^ (t & 3)) : lane)];
 #pragma unroll
                 for (int u = 0; u < NQT; ++u) o[t][u] = mfma16(af, pb[hf][u], o[t][u]);
             }
