@@ -459,7 +459,7 @@ def main():
                    "heads": 32, "kv_heads": 8, "head_dim": 128, "context": 4096, "layers": c2["layers"],
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(c2["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(c2["frac"], 4), "traffic": traffic_from_profiles("attn_decode_c2_counters.md"),
+                     "frac": round(c2["frac"], 4), "traffic": traffic_from_profiles("attn_decode_c2.md"),
                      "kernel": "attn_decode_kernel<128, KV_T16> (split merge by the last-arriving workgroup, one kernel per launch)",
                      "bytes_per_launch": c2["bytes_per_launch"],
                      "us_per_launch": round(c2["us_per_launch"], 3)},
