@@ -96,11 +96,8 @@ int llmtie_supports_flash(size_t head_dim, size_t heads, size_t kv_heads);
 /* Gpu::flash_attn (device.rs:5702): causal or full attention of tq query rows
  * (positions past .. past+tq-1) against an f32 cache holding past+tq keys.
  * out = [tq, heads*head_dim] f32.
- * It stages the f32 keys and values as a tiled f16
- * copy in a library-owned workspace, one per (device, stream), grown on demand
- * and never freed before the process ends. Calls ordered on one stream share
- * it; a HIP graph captured from a stream uses that stream's workspace, so its
- * replays must not overlap other calls made on the capturing stream. */
+ * The kernel rounds the f32 keys and values to f16 on their way into its
+ * LDS tiles (the reference's arithmetic); nothing is allocated. */
 int llmtie_flash_attn(void* stream, const float* q, size_t q_len, const float* k, size_t k_len,
                       const float* v, size_t v_len, float* out, size_t out_len, size_t tq, size_t past,
                       size_t heads, size_t kv_heads, size_t head_dim, size_t cap, float scale, int causal);
@@ -112,8 +109,8 @@ int llmtie_flash_attn_f16(void* stream, const float* q, size_t q_len, const uint
 
 /* Gpu::flash_attn_rows (device.rs:5812): non-causal attention over a stacked
  * [t, 3*heads*head_dim] q/k/v product, scale on q, context as f16 bits
- * [t, heads*head_dim]. head_dim 64. Runs the register-staged kernel on the
- * rows as they lie (no workspace). */
+ * [t, heads*head_dim]. head_dim 64. The rows are read where they lie and
+ * rounded to f16 inside the kernel; nothing is allocated. */
 int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint16_t* out, size_t out_len,
                            size_t t, size_t heads, size_t head_dim, float scale);
 
