@@ -40,6 +40,10 @@ CASES = [
     # at head_dim 64, not a power of two.
     (12, 4, 64, 3000, 3008, True, False),
     (6, 2, 128, 5000, 5056, True, False),
+    # f32 caches at head_dim 128 (not in kernels.rs): group 1 on the VALU,
+    # group 4 on the MFMA path with one block in flight per wave.
+    (4, 4, 128, 300, 320, False, True),
+    (8, 2, 128, 1000, 1024, False, False),
 ]
 
 

@@ -128,3 +128,35 @@ def test_the_encoder_attention_off_its_rows_is_the_split_path(gpu, t, heads, sta
                          "(test_the_encoder_attention_off_its_rows_is_the_split_path, test_c4_whisper_encoder).")
 def test_the_removed_tiled_copy_encoder_route():
     raise AssertionError("this route no longer exists")
+
+
+@pytest.mark.parametrize("heads,kv,hd,causal,tq,past,cap,tiled", [
+    (32, 8, 128, True, 700, 0, 704, True), (32, 8, 128, True, 300, 37, 352, False),
+    (8, 4, 64, True, 257, 0, 258, False), (8, 4, 64, False, 190, 11, 224, True),
+    (6, 6, 128, True, 333, 5, 352, True), (4, 4, 64, False, 500, 0, 500, False),
+    (32, 8, 128, False, 64, 0, 64, True), (16, 2, 128, True, 1, 60, 64, False)])
+def test_the_ping_pong_prefill_is_the_single_group_one(gpu, heads, kv, hd, causal, tq, past, cap, tiled,
+                                                       monkeypatch):
+    """The eight-wave ping-pong kernel (long prefills) runs the same
+    arithmetic in the same order as the four-wave kernel: forced onto these
+    shapes (ragged row counts, a past, causal and full, GQA groups 1/2/4/8,
+    both f16 layouts) it must give the same bits."""
+    from ttsxabe_amd.gpu import TiledCache16
+    tk = past + tq
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    q = up(oracle.seq(tq * heads * hd, 81) * np.float32(4.0))
+    kc, vc = caches(oracle.seq(kv * tk * hd, 82), oracle.seq(kv * tk * hd, 83), kv, tk, cap, hd)
+    k16, v16 = up_f16(kc), up_f16(vc)
+    if tiled:
+        t = TiledCache16(kv, hd, cap, zero=False)
+        t.data.fill_(float("nan"))
+        gpu.t16_from_ref(k16, v16, t, tk)
+        run = lambda: gpu.flash_attn_t16(q, t, tq, past, heads, scale, causal)
+    else:
+        run = lambda: gpu.flash_attn_f16(q, k16, v16, tq, past, heads, kv, hd, cap, scale, causal)
+    monkeypatch.setenv("LLMTIE_PREFILL_PP", "0")
+    want = down(run())
+    monkeypatch.setenv("LLMTIE_PREFILL_PP", "1")
+    got = down(run())
+    assert np.isfinite(got).all()
+    assert np.array_equal(want.view(np.uint32), got.view(np.uint32))

@@ -779,7 +779,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const int nf = nfull > first ? min(nit, (nfull - first + DW - 1) / DW) : 0;
     const bool tail = (tk & 31) && nfull >= first && (nfull - first) % DW == 0 && (nfull - first) / DW < nit;
     FR f0, f1;
-    auto ld = [&](int p, FR& f, auto full_tag) {
+    auto ld = [&](int p, FR& f, auto full_tag) __attribute__((always_inline)) {
         constexpr bool FULL = decltype(full_tag)::value;
         if constexpr (G1 && KIND == KV_F32) load_block_f32v<HD, VA, FULL>(c, p, lane, f);
         else load_block<HD, KIND, VA, FULL>(c, p, lane, f);
@@ -788,7 +788,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     // first use waits for every load issued before them, so a block issued
     // after that would start a second memory round trip.
     if (nf > 0) ld(first * 32, f0, std::true_type{});
-    if (nf > 1) ld((first + DW) * 32, f1, std::true_type{});
+    if (nf > 1 && !(KIND == KV_F32 && HD == 128)) ld((first + DW) * 32, f1, std::true_type{});
 
     // The group's queries as B operands, hi + lo (columns past the group are
     // read from column 0 and zeroed, so every load is unconditional). The
@@ -830,7 +830,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         o[t] = zero_f4();
         o1[t] = 0.0f;
     }
-    auto fold = [&](const FR& f, int p, auto mask_tag) {
+    auto fold = [&](const FR& f, int p, auto mask_tag) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
         if constexpr (G1)
             fold_block_g1<HD, KIND, MASK>(f, qv, p, tk, col, grp, m_run, l_run, o1, prow[wave]);
@@ -846,8 +846,17 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     // own block. The scheduling barriers keep each prefetch ahead of the fold
     // it is meant to overlap (left alone, the scheduler sinks loads towards
     // their uses).
+    // f32 caches at head_dim 128: one block in flight (two would not fit in
+    // the register file and would spill to scratch).
+    constexpr bool DEEP = !(KIND == KV_F32 && HD == 128);
     int i = 0;
-    for (; i + 2 < nf; i += 2) {
+    if constexpr (!DEEP) {
+        for (; i < nf; ++i) {
+            if (i > 0) ld((first + i * DW) * 32, f0, std::true_type{});
+            fold(f0, (first + i * DW) * 32, std::false_type{});
+        }
+    }
+    for (; DEEP && i + 2 < nf; i += 2) {
         const int p0 = (first + i * DW) * 32;
         const int p1 = (first + (i + 1) * DW) * 32;
         const int p2 = (first + (i + 2) * DW) * 32;
@@ -862,8 +871,8 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         __builtin_amdgcn_sched_barrier(0);
     }
     // The last one or two blocks (already in f0, f1).
-    if (i < nf) fold(f0, (first + i * DW) * 32, std::false_type{});
-    if (i + 1 < nf) fold(f1, (first + (i + 1) * DW) * 32, std::false_type{});
+    if (DEEP && i < nf) fold(f0, (first + i * DW) * 32, std::false_type{});
+    if (DEEP && i + 1 < nf) fold(f1, (first + (i + 1) * DW) * 32, std::false_type{});
     if (tail) {
         ld(nfull * 32, f0, std::integral_constant<bool, TILED>{});
         fold(f0, nfull * 32, std::true_type{});
@@ -935,7 +944,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const size_t head = (size_t)seq * a.kv_heads + h;
     float* po = a.part + (head * a.splits) * n;
     float* pml = a.part + a.ml_off + head * a.ml_stride;
-    auto partial4 = [&](int e4) {
+    auto partial4 = [&](int e4) __attribute__((always_inline)) {
         const int g = (4 * e4) / HD, d = (4 * e4) % HD;
         float f[DW];
         weights(g, f);
@@ -944,7 +953,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         for (int w = 0; w < DW; ++w) acc += *reinterpret_cast<const floatx4*>(&lds[w * OBW + g * (HD + 4) + d]) * f[w];
         return acc;
     };
-    auto ml = [&](int g) {
+    auto ml = [&](int g) __attribute__((always_inline)) {
         float f[DW];
         const float M = weights(g, f);
         float L = 0.0f;
@@ -1656,8 +1665,8 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
 #define DECODE_INST(HD, KIND, VA, G1) template __global__ void attn_decode_kernel<HD, KIND, VA, G1>(DecodeArgs);
 #define DECODE_INST2(HD, KIND, VA) DECODE_INST(HD, KIND, VA, false) DECODE_INST(HD, KIND, VA, true)
 DECODE_INST2(64, KV_F16, 16) DECODE_INST2(128, KV_F16, 16) DECODE_INST2(64, KV_F16, 8) DECODE_INST2(128, KV_F16, 8)
-DECODE_INST2(64, KV_F32, 16) DECODE_INST(128, KV_F32, 16, false) DECODE_INST2(64, KV_F32, 8)
-DECODE_INST(128, KV_F32, 8, false) DECODE_INST2(64, KV_T16, 16) DECODE_INST2(128, KV_T16, 16)
+DECODE_INST2(64, KV_F32, 16) DECODE_INST2(128, KV_F32, 16) DECODE_INST2(64, KV_F32, 8)
+DECODE_INST2(128, KV_F32, 8) DECODE_INST2(64, KV_T16, 16) DECODE_INST2(128, KV_T16, 16)
 DECODE_INST(64, KV_TQ8, 16, false) DECODE_INST(128, KV_TQ8, 16, false)
 
 template __global__ void attn_decode_sk_kernel<64>(DecodeArgs);
@@ -1689,10 +1698,8 @@ static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_head
     b.grid8 = (int)(grid.x / 8);
     const int esz = kind == KV_F32 ? 4 : 2;
     const int va = (kind == KV_T16 || kind == KV_TQ8) ? 16 : (((long)a.cap * esz) % 16 == 0 ? 16 : 8);
-    // Group 1 (MHA) folds on the VALU, except f32 caches at head_dim 128
-    // (their raw blocks would not fit two deep in registers).
-    const bool g1 = a.group == 1 && kind != KV_TQ8 && !(kind == KV_F32 && hd == 128) &&
-                    !getenv("LLMTIE_DECODE_G1_MFMA");
+    // Group 1 (MHA) folds on the VALU.
+    const bool g1 = a.group == 1 && kind != KV_TQ8 && !getenv("LLMTIE_DECODE_G1_MFMA");
 #define L(HD, KIND, VA, G1)                                                                    \
     if (hd == HD && kind == KIND && va == VA && g1 == G1) {                                    \
         hipLaunchKernelGGL((attn_decode_kernel<HD, KIND, VA, G1>), grid, block, 0, st, b);      \
@@ -1700,7 +1707,7 @@ static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_head
     }
 #define L2(HD, KIND, VA) L(HD, KIND, VA, false) L(HD, KIND, VA, true)
     L2(64, KV_F16, 16) L2(128, KV_F16, 16) L2(64, KV_F16, 8) L2(128, KV_F16, 8)
-    L2(64, KV_F32, 16) L(128, KV_F32, 16, false) L2(64, KV_F32, 8) L(128, KV_F32, 8, false)
+    L2(64, KV_F32, 16) L2(128, KV_F32, 16) L2(64, KV_F32, 8) L2(128, KV_F32, 8)
     L2(64, KV_T16, 16) L2(128, KV_T16, 16) L(64, KV_TQ8, 16, false) L(128, KV_TQ8, 16, false)
 #undef L2
 #undef L

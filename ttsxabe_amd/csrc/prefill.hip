@@ -475,7 +475,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     static_assert(KIND != PF_ROWS || (HD == 64 && KF % PW == 0 && VF * 64 * 8 == PT * 16), "rows: hd 64");
     constexpr int KI = KF / PW;  // staging slots holding K fragments
     const int rdq = tid & 15, rkq = tid >> 4;  // rows V: dims 4*rdq .. +3, keys 4*rkq .. +3
-    auto stage_load = [&](int kv0) {
+    auto stage_load = [&](int kv0) __attribute__((always_inline)) {
         if constexpr (KIND == PF_ROWS) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -499,25 +499,28 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
                 } else {
                     const int fv = f - KF, hf = fv / NT, t = fv % NT;
                     const int d = 16 * t + col, k0 = kv0 + 32 * hf + 8 * grp;
-                    float x[8];
-                    if (KIND == PF_F32 && vvec && k0 + 8 <= ktot) {
+                    float4 v0, v1;
+                    if (vvec && k0 + 8 <= ktot) {
                         const float4* p = reinterpret_cast<const float4*>(vf32 + svb + (size_t)d * a.cap + k0);
-                        sr[i][0] = p[0];
-                        sr[i][1] = p[1];
-                        continue;
-                    }
+                        v0 = p[0];
+                        v1 = p[1];
+                    } else {
+                        float x[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int key = min(k0 + j, ktot - 1);
-                        x[j] = k0 + j < ktot ? vf32[svb + (size_t)d * a.cap + key] : 0.0f;
+                        for (int j = 0; j < 8; ++j) {
+                            const int key = min(k0 + j, ktot - 1);
+                            x[j] = k0 + j < ktot ? vf32[svb + (size_t)d * a.cap + key] : 0.0f;
+                        }
+                        v0 = make_float4(x[0], x[1], x[2], x[3]);
+                        v1 = make_float4(x[4], x[5], x[6], x[7]);
                     }
-                    sr[i][0] = make_float4(x[0], x[1], x[2], x[3]);
-                    sr[i][1] = make_float4(x[4], x[5], x[6], x[7]);
+                    sr[i][0] = v0;
+                    sr[i][1] = v1;
                 }
             }
         }
     };
-    auto stage_store = [&](half_t* dst) {
+    auto stage_store = [&](half_t* dst) __attribute__((always_inline)) {
         if constexpr (KIND == PF_ROWS) {
             // Dim 4*rdq + e, keys 4*rkq .. +3: V fragment (half, t) = (rkq / 8,
             // dim / 16), lane (dim % 16) + 16 * ((rkq % 8) / 2), halves 4 * (rkq % 2) ..
@@ -551,7 +554,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
         }
     };
 
-    auto issue = [&](int kv0, half_t* dst) {
+    auto issue = [&](int kv0, half_t* dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int f = wave + PW * i;
@@ -633,7 +636,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
 
     // One 64-key tile from LDS buffer `tb`; MASK: some key of it lies past
     // some row's limit.
-    auto tile = [&](const half_t* tb, int kv0, auto mask_tag) {
+    auto tile = [&](const half_t* tb, int kv0, auto mask_tag) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
         const half8* kf = reinterpret_cast<const half8*>(tb);
         const half8* vf = reinterpret_cast<const half8*>(tb + KF * FH);
@@ -735,7 +738,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     };
     // Zero the V entries of keys >= ktot in a tile that reaches past ktot.
-    auto zero_tail = [&](half_t* tb, int kv0) {
+    auto zero_tail = [&](half_t* tb, int kv0) __attribute__((always_inline)) {
         half8* vf = reinterpret_cast<half8*>(tb + KF * FH);
         for (int c = tid; c < VF * 64; c += PT) {
             const int hf = c / (NT * 64), ln = c % 64;
@@ -749,7 +752,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
             }
         }
     };
-    auto step = [&](half_t* cur, half_t* nxt, int kv0) {
+    auto step = [&](half_t* cur, half_t* nxt, int kv0) __attribute__((always_inline)) {
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of `cur` have landed
         __syncthreads();                 // ... and every wave's; `nxt` is free
         if (kv0 + KT < kend) issue(kv0 + KT, nxt);
@@ -768,7 +771,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     // tile j + 1's f32 loads are in flight in registers while tile j is
     // computed, then rounded and written to `nxt`, which every wave finished
     // reading before that barrier.
-    auto step_staged = [&](half_t* cur, half_t* nxt, int kv0) {
+    auto step_staged = [&](half_t* cur, half_t* nxt, int kv0) __attribute__((always_inline)) {
         __syncthreads();
         const bool more = kv0 + KT < kend;
         if (more) stage_load(kv0 + KT);
@@ -818,6 +821,311 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------
+// Long prefills: the f16-cache kernel in "ping-pong" form. A workgroup is
+// eight waves in two groups of four (A: waves 0-3, B: waves 4-7); waves w and
+// w + 4 share a SIMD. Both groups hold 32 query rows per wave (two 16-row
+// tiles) and share each 64-key K/V tile in LDS. Per tile a wave's work is
+// S = K Q^T (MFMA), the softmax (VALU) and O += V^T P^T (MFMA). Between two
+// workgroup barriers (one tile period) group A computes PV(q - 1), S(q) and
+// then softmax(q), group B softmax(q - 1) and then PV(q - 1), S(q), so the
+// two waves of each SIMD start every period in opposite units and the
+// softmax of one overlaps the MFMAs of the other (in the four-wave kernel
+// the two waves of a SIMD come from different workgroups, drift into the
+// same phase, and VALU issues beside MFMAs in only ~22 % of MFMA cycles).
+// The arithmetic per row is the four-wave kernel's, in the same order, so
+// the results are bit-identical. (A stricter version, a barrier at every
+// phase change, raised the co-issue by half but lost more to the barrier
+// waits of a whole compute unit: C3 at 8192 rows 634 vs 612 µs.)
+//
+// Tiles rotate through three LDS buffers: period q reads K_q and V_(q-1);
+// tile q + 1 is issued at the start of period q into the buffer of tile
+// q - 2 and waited for at the end of period q.
+constexpr int PPW = 8;  // waves of a ping-pong workgroup
+
+template <int HD, int KIND>
+__global__ __launch_bounds__(PPW * LLMTIE_WAVE, 1) void flash_pp_kernel(PrefillArgs a) {
+    static_assert(KIND == PF_F16 || KIND == PF_T16, "f16 caches");
+    constexpr int NQT = 2;
+    constexpr int NS = HD / 32;
+    constexpr int NT = HD / 16;
+    constexpr int QPW = 16 * NQT;
+    constexpr int KF = 4 * NS;
+    constexpr int VF = 2 * NT;
+    constexpr int FH = 64 * 8;
+    constexpr int NF = (KF + VF) / PPW;  // fragments each wave loads per tile
+    constexpr int TPW = PPW * LLMTIE_WAVE;
+    static_assert((KF + VF) % PPW == 0, "fragments split evenly over the waves");
+    __shared__ __attribute__((aligned(16))) half_t tbuf[3][(KF + VF) * FH];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int gi = wave >> 2;  // 0: group A, 1: group B
+    const int wl = wave & 3;
+    const int gb = a.gb;
+    const int gpr = QPW * (4 / gb);  // rows of one group
+    const int pb = 2 * gpr;          // rows of the workgroup
+    const int group = a.heads / a.kv_heads;
+    int rb = blockIdx.x, gy = blockIdx.y;
+    if (a.xcd) {
+        const int item = (int)(blockIdx.x % 8) * a.grid8 + (int)(blockIdx.x / 8);
+        gy = item / a.nrb;
+        rb = item % a.nrb;
+    }
+    const int bx = a.causal ? a.nrb - 1 - rb : rb;
+    const int h = gy * gb + wl % gb;
+    const int kh = (gy * gb) / group;
+    const int bp0 = bx * pb;
+    const int p0 = bp0 + gi * gpr + (wl / gb) * QPW;
+    const int ktot = a.past + a.tq;
+    const int kend = a.causal ? min(ktot, a.past + bp0 + pb) : ktot;
+    const int wlim = a.causal ? min(a.past + p0 + QPW - 1, ktot - 1) : ktot - 1;
+    const int wall = a.causal ? min(a.past + p0, ktot - 1) : ktot - 1;
+    const int ntile = (kend + KT - 1) / KT;
+
+    const half_t* kc = static_cast<const half_t*>(a.k);
+    const size_t tblk = (size_t)kh * tiled_nblk(a.cap);
+    const int lastb = (max(kend, 1) - 1) >> 5;
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.v), 0, (int)(uint32_t)a.v_bytes, 0x00020000);
+
+    auto issue = [&](int kv0, half_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            const int f = wave + PPW * i;
+            half_t* l = dst + f * FH;
+            if constexpr (KIND == PF_T16) {
+                const int hf = f < KF ? f / (2 * NS) : (f - KF) / NT;
+                const int b = min((kv0 >> 5) + hf, lastb);
+                const int in = f < KF ? (f % (2 * NS)) * FH : 32 * HD + ((f - KF) % NT) * FH;
+                __builtin_amdgcn_global_load_lds(kc + (tblk + b) * (64 * HD) + in + lane * 8, l, 16, 0, 0);
+            } else {
+                if (f < KF) {
+                    const int hf = f / (2 * NS), T = (f / NS) & 1, s = f % NS;
+                    const int key = min(kv0 + 32 * hf + 8 * (col >> 2) + 4 * T + (col & 3), ktot - 1);
+                    __builtin_amdgcn_global_load_lds(kc + ((size_t)kh * a.cap + key) * HD + 32 * s + 8 * grp, l, 16,
+                                                     0, 0);
+                } else {
+                    const int fv = f - KF, hf = fv / NT, t = fv % NT;
+                    const int d = 16 * t + col, key0 = kv0 + 32 * hf + 8 * grp;
+                    const uint32_t off = (uint32_t)((((size_t)kh * HD + d) * a.cap + key0) * 2);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, l, 16, off, 0, 0, 0);
+                }
+            }
+        }
+    };
+    auto zero_tail = [&](half_t* tb, int kv0) __attribute__((always_inline)) {
+        half8* vf = reinterpret_cast<half8*>(tb + KF * FH);
+        for (int c = tid; c < VF * 64; c += TPW) {
+            const int hf = c / (NT * 64), ln = c % 64;
+            const int k0 = kv0 + 32 * hf + 8 * (ln >> 4);
+            if (k0 + 8 > ktot) {
+                half8 x = vf[c];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (k0 + j >= ktot) x[j] = (half_t)0.0f;
+                vf[c] = x;
+            }
+        }
+    };
+
+    // The first three tiles go out before the queries are read.
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+        if (j < ntile) issue(j * KT, tbuf[j]);
+    const float qsc = a.scale_q ? a.scale : 1.0f;
+    half8 qb[NQT][NS];
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        const int r = min(p0 + 16 * u + col, a.tq - 1);
+        const float m = p0 + 16 * u + col < a.tq ? qsc : 0.0f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const float4* p = reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 32 * s + 8 * grp);
+            const float4 x0 = p[0], x1 = p[1];
+            half8 x;
+            x[0] = to_h(x0.x * m); x[1] = to_h(x0.y * m); x[2] = to_h(x0.z * m); x[3] = to_h(x0.w * m);
+            x[4] = to_h(x1.x * m); x[5] = to_h(x1.y * m); x[6] = to_h(x1.z * m); x[7] = to_h(x1.w * m);
+            qb[u][s] = x;
+        }
+    }
+    floatx4 o[NT][NQT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) o[t][u] = zero_f4();
+    float m[NQT], l[NQT];
+    int ilim[NQT];
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        m[u] = ninf();
+        l[u] = 0.0f;
+        const int r = p0 + 16 * u + col;
+        ilim[u] = a.causal ? min(a.past + r, ktot - 1) : ktot - 1;
+    }
+    const float sl2 = (a.scale_q ? 1.0f : a.scale) * LLMTIE_LOG2E;
+    constexpr float RB = 8.0f;
+    floatx4 sc[2][2][NQT];
+    half8 pb2[2][NQT];
+
+    auto scores = [&](const half_t* tb) __attribute__((always_inline)) {
+        const half8* kf = reinterpret_cast<const half8*>(tb);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+#pragma unroll
+                for (int u = 0; u < NQT; ++u) sc[hf][T][u] = zero_f4();
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const half8 af = kf[((hf * 2 + T) * NS + s) * 64 + lane];
+#pragma unroll
+                    for (int u = 0; u < NQT; ++u) sc[hf][T][u] = mfma16(af, qb[u][s], sc[hf][T][u]);
+                }
+            }
+        {
+            constexpr int NR = 4 * NS, PD = LLMTIE_PF_PD < NR ? LLMTIE_PF_PD : NR;
+            __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
+#pragma unroll
+            for (int i2 = 0; i2 < NR - PD; ++i2) {
+                __builtin_amdgcn_sched_group_barrier(0x008, NQT, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NQT * PD, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto values = [&](const half_t* tb) __attribute__((always_inline)) {
+        const half8* vf = reinterpret_cast<const half8*>(tb + KF * FH);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const half8 af = vf[(hf * NT + t) * 64 + lane];
+#pragma unroll
+                for (int u = 0; u < NQT; ++u) o[t][u] = mfma16(af, pb2[hf][u], o[t][u]);
+            }
+        {
+            constexpr int NR = 2 * NT, PD = LLMTIE_PF_PD < NR ? LLMTIE_PF_PD : NR;
+            __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
+#pragma unroll
+            for (int i2 = 0; i2 < NR - PD; ++i2) {
+                __builtin_amdgcn_sched_group_barrier(0x008, NQT, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NQT * PD, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto softmax = [&](int kv0, auto mask_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) {
+            float mx = ninf();
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if constexpr (MASK) {
+                            const int key = kv0 + 32 * hf + 8 * grp + 4 * T + r;
+                            sc[hf][T][u][r] = key <= ilim[u] ? sc[hf][T][u][r] : ninf();
+                        }
+                        mx = fmaxf(mx, sc[hf][T][u][r]);
+                    }
+            mx = max4grp(mx) * sl2;
+            if (__any(mx > m[u] + RB)) {
+                const float mn = fmaxf(m[u], mx);
+                const float fac = mn == ninf() ? 1.0f : ex2(m[u] - mn);
+                m[u] = mn;
+                l[u] *= fac;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) o[t][u] *= fac;
+            }
+            const float msub = m[u] == ninf() ? 0.0f : m[u];
+            float ps = 0.0f;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                half8 p;
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = ex2(__builtin_fmaf(sc[hf][T][u][r], sl2, -msub));
+                        ps += e;
+                        p[4 * T + r] = to_h(e);
+                    }
+                pb2[hf][u] = p;
+            }
+            l[u] += ps;
+        }
+    };
+
+    if (ntile > 0) {
+        __builtin_amdgcn_s_waitcnt(0);
+        if (KT > ktot) zero_tail(tbuf[0], 0);
+    }
+    __syncthreads();
+    auto smax = [&](int j) __attribute__((always_inline)) {
+        if (j * KT + KT - 1 > wall)
+            softmax(j * KT, std::true_type{});
+        else
+            softmax(j * KT, std::false_type{});
+    };
+    {
+        // One barrier per tile period q: K_q and V_(q-1) are read. Group A
+        // computes PV(q - 1), S(q) then softmax(q); group B softmax(q - 1)
+        // then PV(q - 1), S(q): the two waves of a SIMD start each period in
+        // opposite units. Tile q + 1 is issued at the start of period q into
+        // the buffer of tile q - 2 (last read in period q - 1) and waited for
+        // at its end; V past ktot of tile q is zeroed in period q, before
+        // period q + 1 reads it.
+        for (int q = 0; q <= ntile; ++q) {
+            if (q >= 2 && q + 1 < ntile) issue((q + 1) * KT, tbuf[(q + 1) % 3]);
+            if (q >= 1 && q < ntile && q * KT + KT > ktot) zero_tail(tbuf[q % 3], q * KT);
+            if (gi == 0) {
+                if (q >= 1 && (q - 1) * KT <= wlim) values(tbuf[(q - 1) % 3]);
+                if (q < ntile && q * KT <= wlim) {
+                    scores(tbuf[q % 3]);
+                    smax(q);
+                }
+            } else {
+                if (q >= 1 && (q - 1) * KT <= wlim) {
+                    smax(q - 1);
+                    values(tbuf[(q - 1) % 3]);
+                }
+                if (q < ntile && q * KT <= wlim) scores(tbuf[q % 3]);
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // the tile issued at the start of this period
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NQT; ++u) {
+        const float lt = sum4grp(l[u]);
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const int r = p0 + 16 * u + col;
+        if (r >= a.tq) continue;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const size_t off = (size_t)r * a.os + (size_t)h * HD + 16 * t + 4 * grp;
+            if (a.out_f16) {
+                half4 y;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) y[k] = to_h(o[t][u][k] * inv);
+                *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(a.out) + off) = y;
+            } else {
+                float4 y = make_float4(o[t][u][0] * inv, o[t][u][1] * inv, o[t][u][2] * inv, o[t][u][3] * inv);
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + off) = y;
+            }
+        }
+    }
+}
+
 hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st) {
     const int pb = 16 * nqt * (PW / a.gb);
     dim3 grid((a.tq + pb - 1) / pb, a.heads / a.gb), block(PT);
@@ -836,6 +1144,29 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
     const bool f32ok = (kind == PF_F32 && al16) || (kind == PF_ROWS && al16 && a.kvs % 4 == 0);
     const bool fast = (kind == PF_T16 || (kind == PF_F16 && a.v_bytes <= 0xffffffffull) || f32ok) &&
                       (a.scale_q || a.scale > 0.0f) && !getenv("LLMTIE_PREFILL_STAGED");
+    // Long prefills of an f16 cache: the ping-pong kernel, once its 64-row
+    // workgroups still fill the chip (LLMTIE_PREFILL_PP=0 turns it off, =1
+    // forces it where it applies).
+    const char* ppe = getenv("LLMTIE_PREFILL_PP");
+    const int pp_rows = 2 * 32 * (4 / a.gb);
+    const unsigned pp_items = (unsigned)((a.tq + pp_rows - 1) / pp_rows) * (unsigned)(a.heads / a.gb);
+    const bool pp = fast && (kind == PF_T16 || kind == PF_F16) && !(ppe && !atoi(ppe)) &&
+                    ((ppe && atoi(ppe)) || pp_items >= 1024);
+    if (pp) {
+        PrefillArgs b = a;
+        b.nrb = (a.tq + pp_rows - 1) / pp_rows;
+        b.xcd = pp_items % 8 == 0 && !(getenv("LLMTIE_PREFILL_XCD") && !atoi(getenv("LLMTIE_PREFILL_XCD")));
+        b.grid8 = (int)(pp_items / 8);
+        const dim3 g = b.xcd ? dim3(pp_items) : dim3(b.nrb, a.heads / a.gb);
+        const dim3 blk(PPW * LLMTIE_WAVE);
+#define PPL(HD, KIND)                                                          \
+    if (hd == HD && kind == KIND) {                                             \
+        hipLaunchKernelGGL((flash_pp_kernel<HD, KIND>), g, blk, 0, st, b);      \
+        return hipGetLastError();                                               \
+    }
+        PPL(64, PF_F16) PPL(128, PF_F16) PPL(64, PF_T16) PPL(128, PF_T16)
+#undef PPL
+    }
     if (fast) {
         PrefillArgs b = a;
         b.nrb = (int)grid.x;
