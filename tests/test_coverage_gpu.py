@@ -6,8 +6,8 @@
   sequence, 64 sequences (the largest device-planned batch), 65 (the
   host-planned grid), and one-position sequences.
 - The prefill's staged fallback for a non-positive score scale.
-- The f32 prefill's per-stream workspace: two streams at once, and a first
-  use inside a captured graph (the stream-ordered fallback).
+- The f32-cache prefill (staged through registers inside the kernel): two
+  streams at once, and a first use inside a captured graph.
 Bars as elsewhere: decode 2e-5 of full scale against the exact f64 value;
 Q8_0 1e-3 (one f16 rounding of P * d_v); prefill the reference's rule.
 """
@@ -73,6 +73,7 @@ def test_prefill_with_a_non_positive_scale_takes_the_staged_path(gpu, scale):
 
 
 def test_f32_prefill_on_two_streams_at_once(gpu):
+    # Two f32-cache prefills in flight on two streams share no state.
     hd, heads, kv = 128, 8, 2
     cases = []
     for tq, salt in ((300, 1), (700, 2)):
@@ -94,10 +95,9 @@ def test_f32_prefill_on_two_streams_at_once(gpu):
 
 
 def test_f32_prefill_first_used_inside_a_graph(gpu):
-    # The capturing stream may have no workspace yet (torch pools its
-    # streams, so it may also have one): then the first call happens under
-    # capture and the copy is allocated and freed inside the graph. Either
-    # way every replay must equal the eager result.
+    # The f32 cache is staged inside the kernel (nothing is allocated), so a
+    # first call made under capture is an ordinary kernel node: every replay
+    # must equal the eager result.
     hd, heads, kv, tq = 64, 4, 4, 1000
     q = up(oracle.seq(tq * heads * hd, 71) - 2.0)
     k = up(oracle.seq(kv * tq * hd, 72))
