@@ -1370,6 +1370,8 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     half8 qh[NS], ql[NS];
     float m_run = ninf(), l_run = 0.0f;
     floatx4 o[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) o[t] = zero_f4();  // finite from the start (see the segment start)
     // Pending partial publications (slot 0, slot 1): the head's flat start
     // position, or -1.
     long pend0 = -1, pend1 = -1;
@@ -1411,10 +1413,12 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
                     ql[s][j] = ll;
                 }
             }
+            // The previous segment's context is already written: with m at
+            // -inf the fold's rescale factor 2^(m - M) is exactly 0 and
+            // clears o (always finite). An explicit reset here made the
+            // compiler carry o through AGPRs, 64 moves a block.
             m_run = ninf();
             l_run = 0.0f;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) o[t] = zero_f4();
         }
         // The slot (and the query buffer) are read: refill the slot with the
         // block two ahead.
