@@ -42,8 +42,10 @@ def hipcc() -> str:
 # Per-source extra flags. The prefill kernels' softmax takes maxima of raw
 # MFMA outputs; with NaNs honoured every fmaxf operand first gets a
 # canonicalising v_max of its own. Infinities (the -inf of masked keys)
-# stay honoured.
-EXTRA = {"prefill.hip": ["-fno-honor-nans"]}
+# stay honoured. The decode kernels' MFMAs write VGPRs: in the AGPR form the
+# batched Q8_0 kernel kept its context in AGPRs for the MFMAs and in VGPRs
+# across the loop, 64 register moves a block (C5 68.6 -> 66.3 us).
+EXTRA = {"prefill.hip": ["-fno-honor-nans"], "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 COMPILE = [f for f in FLAGS if f != "-shared"]
 
 
