@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the fused-attention hot path on one MI355X.
 
-Headline (BASELINE.json `metric`, configs[1]): Llama-3-8B GQA decode
+Headline (the benchmark metric, config C2): Llama-3-8B GQA decode
 (32 query / 8 KV heads, head_dim 128, 4096-position f16 cache, batch 1). A
 step is one decoded token through a 32-layer stack: 32 decode-attention
 launches, each over its own layer's KV cache, so the 537 MB touched per step

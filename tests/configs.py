@@ -1,4 +1,4 @@
-"""The BASELINE.json configs as seeded synthetic workloads (shared by the
+"""The five benchmark configs C1-C5 as seeded synthetic workloads (shared by the
 config parity tests, smoke() and bench.py). Inputs come from the oracle's
 counter-based generators, so any rank or test regenerates them bit-exactly.
 """

@@ -1,4 +1,4 @@
-"""The BASELINE.json configs at full size against the oracle, at the north
+"""The benchmark configs C1-C5 at full size against the oracle, at the north
 star's bar: max |err| <= 5e-3 and per-head cosine >= 0.9999 (tolerances
 written here), plus the reference's own per-element prefill rule where the
 f64 reference applies.
