@@ -1533,11 +1533,10 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     // its max M is taken once, and every contributor then adds 2^(m - M)
     // times its l and O. The arithmetic of a head depends only on its own
     // contributors, never on which wave merges it or what it merges beside.
-    // O moves in batches of MB contributors (both heads' chunks as one
-    // list), two float4 loads each: with the (m, l) loads at most ~60
+    // O moves in batches of MB = 8 or 24 contributors (both heads' chunks as
+    // one list), two float4 loads each: with the (m, l) loads at most ~60
     // vector-memory instructions, under the 63 a wave can have outstanding.
     // Lane owns float4 e4 = lane + 64 j of a head's [g][HD] context.
-    constexpr int MB = 24;
     constexpr int HALF_F = ((2 * BB / 4 - 64) / 2) / 64 * 64;  // floats of LDS per head
     const int gp = 2 * group;                            // (m, l) floats per contributor
     const int KC = HALF_F / gp;
@@ -1571,7 +1570,8 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
                     __builtin_amdgcn_global_load_lds(src, mls + hh * HALF_F + 64 * i, 4, 0, AUX_AGENT);
                 }
             }
-            for (int cb = 0; cb < nc; cb += MB) {
+            auto batch = [&](auto mbc, int cb) __attribute__((always_inline)) {
+                constexpr int MB = decltype(mbc)::value;
                 float4 ov[MB][2];
 #pragma unroll
                 for (int k = 0; k < MB; ++k) {
@@ -1632,22 +1632,37 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
 #pragma unroll
                     for (int j = 0; j < 2; ++j) mv[k][j] = *reinterpret_cast<const float2*>(ml + 2 * g[j]);
                 }
+                // Explicit fmaf: the rounding is the same in either batch
+                // size. A contributor adds to its own head and adds weight 0
+                // (an exact +0) to the other, so no register array is
+                // indexed at run time.
 #pragma unroll
                 for (int k = 0; k < MB; ++k) {
                     const int e = cb + k;
-                    if (e >= nc) continue;
-                    const int hb = e >= nA ? 1 : 0;
+                    if (e >= nc) break;
+                    const bool inA = e < nA;
 #pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        if (hh != hb) continue;
-#pragma unroll
-                        for (int j = 0; j < 2; ++j) {
-                            L[hh][j] += mv[k][j].y;
-                            acc[hh][j] += floatx4{ov[k][j].x, ov[k][j].y, ov[k][j].z, ov[k][j].w} * mv[k][j].x;
-                        }
+                    for (int j = 0; j < 2; ++j) {
+                        const float w = mv[k][j].x, lw = mv[k][j].y;
+                        const float wa = inA ? w : 0.0f, wb = inA ? 0.0f : w;
+                        L[0][j] += inA ? lw : 0.0f;
+                        L[1][j] += inA ? 0.0f : lw;
+                        acc[0][j][0] = __builtin_fmaf(ov[k][j].x, wa, acc[0][j][0]);
+                        acc[0][j][1] = __builtin_fmaf(ov[k][j].y, wa, acc[0][j][1]);
+                        acc[0][j][2] = __builtin_fmaf(ov[k][j].z, wa, acc[0][j][2]);
+                        acc[0][j][3] = __builtin_fmaf(ov[k][j].w, wa, acc[0][j][3]);
+                        acc[1][j][0] = __builtin_fmaf(ov[k][j].x, wb, acc[1][j][0]);
+                        acc[1][j][1] = __builtin_fmaf(ov[k][j].y, wb, acc[1][j][1]);
+                        acc[1][j][2] = __builtin_fmaf(ov[k][j].z, wb, acc[1][j][2]);
+                        acc[1][j][3] = __builtin_fmaf(ov[k][j].w, wb, acc[1][j][3]);
                     }
                 }
-            }
+            };
+            // Most merges hold at most 8 contributors: a batch of 8 keeps
+            // their loads, LDS reads and folds to what they use.
+            if (nc <= 8) batch(std::integral_constant<int, 8>{}, 0);
+            else
+                for (int cb = 0; cb < nc; cb += 24) batch(std::integral_constant<int, 24>{}, cb);
         }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
