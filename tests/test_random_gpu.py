@@ -1,0 +1,77 @@
+"""Seeded random shapes through the three hot entries, against the oracle.
+
+The named cases elsewhere mirror the reference's own tests
+(crates/llmtie-cuda/tests/kernels.rs:2782-2937 for decode, :2249-2375 for
+the fused prefill); these add shapes drawn at random from a fixed seed, so a
+plan edge the named cases miss (a split count, a ragged block, a batch with
+repeated slots) still meets the same bars: decode within 2e-5 of full scale
+of the exact f64 attention (kernels.rs:2907-2914), the batched Q8_0 decode
+within 1e-3 of it on the dequantised cache (it has no reference path), and
+the prefill within the reference's per-element rule (kernels.rs:2352-2370).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.test_prefill_gpu import fused_attention_sized
+from tests.test_q8_decode_gpu import check_batch
+from tests.util import down, full_scale_err, up, up_f16
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(32, 8), (8, 8), (16, 2), (20, 20), (12, 4), (8, 1)]
+
+
+def draw(seed):
+    rng = np.random.default_rng(seed)
+    heads, kv = SHAPES[rng.integers(len(SHAPES))]
+    hd = int(rng.choice([64, 128]))
+    return rng, heads, kv, hd
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_f16_decode(gpu, seed):
+    from ttsxabe_amd.gpu import DecodeScratch, TiledCache16
+    rng, heads, kv, hd = draw(1000 + seed)
+    cap = int(rng.integers(1, 1200)) * 4          # f16 rows stay 8-byte aligned
+    tk = int(rng.integers(1, cap + 1))
+    scale_q = bool(rng.integers(2))
+    q = oracle.normal(heads * hd, 2000 + seed)
+    k0 = oracle.normal(kv * cap * hd, 3000 + seed)
+    v0 = oracle.normal(kv * hd * cap, 4000 + seed)
+    k, v = oracle.through_f16(k0), oracle.through_f16(v0)
+    scale = hd ** -0.5
+    s = DecodeScratch()
+    dk, dv = up_f16(k0), up_f16(v0)
+    a = down(gpu.attn_decode_f16(up(q), dk, dv, heads, kv, hd, tk, cap, scale, scale_q, s))
+    t = TiledCache16(kv, hd, cap)
+    gpu.t16_from_ref(dk, dv, t, tk)
+    b = down(gpu.attn_decode_t16(up(q), t, heads, tk, scale, scale_q, s))
+    assert np.array_equal(a, b), "tiled cache differs from the reference layout"
+    exact = oracle.decode_f64(q, k, v, heads, kv, hd, tk, cap, scale, scale_q)
+    err = full_scale_err(exact, a)
+    assert err < 2e-5, f"{(heads, kv, hd, tk, cap, scale_q)}: {err:.3e} of full scale"
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_q8_batch_decode(gpu, seed):
+    rng, heads, kv, hd = draw(5000 + seed)
+    if heads // kv > 16:
+        heads = kv * 16
+    cap = int(rng.choice([32, 64, 256, 1024]))
+    nseq = int(rng.integers(1, 65))
+    slots = int(rng.integers(1, nseq + 1))
+    tk = rng.integers(1, cap + 1, size=nseq).astype(np.int32)
+    slot = rng.integers(0, slots, size=nseq).astype(np.int32)   # repeats allowed
+    check_batch(gpu, hd, heads, kv, slots, cap, tk, slot, 6000 + seed, scale_q=bool(rng.integers(2)))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_prefill(gpu, seed):
+    rng, heads, kv, hd = draw(7000 + seed)
+    causal = bool(rng.integers(2))
+    tq = int(rng.integers(1, 400))
+    past = int(rng.integers(0, 100))
+    cap = (past + tq + int(rng.integers(0, 64)) + 7) // 8 * 8   # rows of whole 16-byte f16 chunks
+    fused_attention_sized(gpu, heads, kv, hd, causal, tq, past, cap, bool(rng.integers(2)))
