@@ -2,8 +2,9 @@
 the program's own eager work and synchronisations between replays, must give
 the eager result bit for bit. Covers the decode's split hand-off (arrival
 counters left at zero by every call, so a replay starts clean), the two-phase
-merge, the prefill (f16 caches, and the f32 sources staged inside the
-kernel), and the decode scratch's growth around a captured graph."""
+merge, the batched Q8_0 decode, the prefill (f16 caches, and the f32
+sources staged inside the kernel), and the decode scratch's growth around a
+captured graph."""
 import os
 
 import numpy as np
@@ -63,6 +64,22 @@ def test_prefill_graph_replays(gpu):
     v32 = up(oracle.seq(kv * cap * hd, 6))
     _replays_match(lambda: [gpu.flash_attn_f16(q, k16, v16, tq, 0, heads, kv, hd, cap, 0.088, True),
                             gpu.flash_attn(q, k32, v32, tq, 0, heads, kv, hd, cap, 0.088, True)])
+
+
+def test_batched_q8_decode_graph_replays(gpu):
+    """The stream-K decode: its mergers leave the arrival counters at zero
+    in the kernel, so every replay starts clean (scratch grown by the eager
+    call first)."""
+    from ttsxabe_amd.gpu import DecodeScratch, KvCacheQ8
+    from tests.test_q8_decode_gpu import load, random_q8_cache
+    hd, heads, kv, slots, cap = 128, 32, 8, 6, 1024
+    cache = KvCacheQ8(slots, kv, hd, cap)
+    load(cache, *random_q8_cache(slots, kv, hd, cap, 31))
+    tk = up(np.array([1000, 33, 517, 1024, 260], np.int32), torch.int32)
+    slot = up(np.array([5, 0, 2, 2, 3], np.int32), torch.int32)
+    q = up(oracle.normal(5 * heads * hd, 32))
+    s = DecodeScratch()
+    _replays_match(lambda: [gpu.attn_decode_q8_batch(q, cache, tk, slot, 1024, heads, hd ** -0.5, False, s)])
 
 
 def test_encoder_rows_graph_replays(gpu):
