@@ -1357,9 +1357,9 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
         char* dst = &ring[wave][slot][0];
 #pragma unroll
         for (int i = 0; i < CODE_I; ++i)
-            __builtin_amdgcn_global_load_lds(src + 1024 * i + 16 * lane, dst + 1024 * i, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src + 1024 * i + 16 * lane, dst + 1024 * i, 16, 0, AUX_STREAM);
         if (lane < SCL_L)
-            __builtin_amdgcn_global_load_lds(src + 64 * HD + 16 * lane, dst + 64 * HD, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src + 64 * HD + 16 * lane, dst + 64 * HD, 16, 0, AUX_STREAM);
         vm_ops += LPB;
         mark[slot] = vm_ops;
         if (pi + 1 < p_end) step(ci);
