@@ -115,12 +115,12 @@ struct Ctx {
 // Eight consecutive V^T elements (one value row, keys kb..kb+7) off the
 // reference layout as f16 hi/lo or exact f16. VA is the alignment the row
 // start guarantees (16 or 8 bytes).
-template <int KIND, int VA>
+template <int KIND, int VA, bool NTL = false>
 __device__ __forceinline__ void v_row8(const Ctx& c, size_t row, half8& h, half8& l) {
     if constexpr (KIND == KV_F16) {
         const uint16_t* p = reinterpret_cast<const uint16_t*>(c.v) + row;
         if constexpr (VA == 16) {
-            h = ld_h8(p);
+            h = NTL ? __builtin_nontemporal_load(reinterpret_cast<const half8*>(p)) : ld_h8(p);
         } else {
             const uint2 a = reinterpret_cast<const uint2*>(p)[0];
             const uint2 b = reinterpret_cast<const uint2*>(p)[1];
@@ -168,13 +168,15 @@ __device__ __forceinline__ uint4 ld_stream16(const uint4* p) {
 // Tiled layouts: straight 16-byte-per-lane reads, always in bounds (a tiled
 // cache holds whole blocks); keys >= tk are dropped later by the fold. Each
 // instruction reads whole 1 KB runs that nothing reads again in the launch,
-// so they are non-temporal (C2 9.86 -> 9.43 us); the reference layouts'
-// 16-byte pieces share lines across instructions and stay ordinary loads
-// (non-temporal, the MHA decode at 4000 positions went 22.1 -> 23.9 us).
+// so they are non-temporal (C2 9.86 -> 9.43 us). The reference layouts'
+// 16-byte pieces are non-temporal (NTL) on the MFMA path (C2 reference
+// layout 10.16 -> 9.94 us) but not on the group-1 path, whose loads share
+// lines in a pattern the evict-first policy hurts (the MHA decode at 4000
+// positions went 22.1 -> 23.9 us).
 // Reference layouts: FULL = every key of the block is live, so nothing is
 // guarded; !FULL = the one partial block at the end of the context, where
 // keys >= tk read as zero and nothing past tk is touched.
-template <int HD, int KIND, int VA, bool FULL>
+template <int HD, int KIND, int VA, bool FULL, bool NTL = false>
 __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<HD, KIND>& f) {
     constexpr int NS = HD / 32;
     constexpr int NT = HD / 16;
@@ -216,7 +218,8 @@ __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<
             for (int s = 0; s < NS; ++s) {
                 const int d0 = 32 * s + 8 * grp;
                 if constexpr (KIND == KV_F16) {
-                    const half8 x = ld_h8(c.k + ((size_t)kk * HD + d0) * 2);
+                    const half8* kp = reinterpret_cast<const half8*>(c.k + ((size_t)kk * HD + d0) * 2);
+                    const half8 x = NTL ? __builtin_nontemporal_load(kp) : *kp;
                     f.k[T][s] = ok ? x : zero_h8();
                 } else {
                     const float4* p = reinterpret_cast<const float4*>(c.k + ((size_t)kk * HD + d0) * 4);
@@ -241,7 +244,7 @@ __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<
             const size_t row = (size_t)(16 * t + col) * c.cap + kb;
             half8 h = zero_h8(), l = zero_h8();
             if constexpr (FULL) {
-                v_row8<KIND, VA>(c, row, h, l);
+                v_row8<KIND, VA, NTL>(c, row, h, l);
             } else {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -793,7 +796,7 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     auto ld = [&](int p, FR& f, auto full_tag) __attribute__((always_inline)) {
         constexpr bool FULL = decltype(full_tag)::value;
         if constexpr (G1 && KIND == KV_F32) load_block_f32v<HD, VA, FULL>(c, p, lane, f);
-        else load_block<HD, KIND, VA, FULL>(c, p, lane, f);
+        else load_block<HD, KIND, VA, FULL, !G1>(c, p, lane, f);
     };
     // The first two blocks go out before the queries are read: the queries'
     // first use waits for every load issued before them, so a block issued
