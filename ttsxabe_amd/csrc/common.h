@@ -60,13 +60,6 @@ __device__ __forceinline__ floatx4 zero_f4() {
 }
 
 // 16 bytes as eight halves; `p` must be 16-byte aligned.
-// A float4 read once in the launch, with the non-temporal hint.
-__device__ __forceinline__ float4 ld_stream_f4(const float4* p) {
-    typedef float v4f __attribute__((ext_vector_type(4)));
-    const v4f x = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
-    return make_float4(x[0], x[1], x[2], x[3]);
-}
-
 __device__ __forceinline__ half8 ld_h8(const void* p) {
     return *reinterpret_cast<const half8*>(p);
 }

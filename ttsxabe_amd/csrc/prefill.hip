@@ -599,11 +599,8 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const float4* p = reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 32 * s + 8 * grp);
-            // The queries are read once: non-temporal for the f16 caches
-            // (C3 at 512 rows 14.1 -> 13.7 us); the staged encoder rows
-            // measured no better that way.
-            qx[u][s][0] = STAGED ? p[0] : ld_stream_f4(p);
-            qx[u][s][1] = STAGED ? p[1] : ld_stream_f4(p + 1);
+            qx[u][s][0] = p[0];
+            qx[u][s][1] = p[1];
         }
     }
     half8 qb[NQT][NS];
@@ -946,7 +943,7 @@ __global__ __launch_bounds__(PPW * LLMTIE_WAVE, 1) void flash_pp_kernel(PrefillA
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const float4* p = reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 32 * s + 8 * grp);
-            const float4 x0 = ld_stream_f4(p), x1 = ld_stream_f4(p + 1);
+            const float4 x0 = p[0], x1 = p[1];
             half8 x;
             x[0] = to_h(x0.x * m); x[1] = to_h(x0.y * m); x[2] = to_h(x0.z * m); x[3] = to_h(x0.w * m);
             x[4] = to_h(x1.x * m); x[5] = to_h(x1.y * m); x[6] = to_h(x1.z * m); x[7] = to_h(x1.w * m);
