@@ -1647,30 +1647,28 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
                     for (int j = 0; j < 2; ++j) mv[k][j] = *reinterpret_cast<const float2*>(ml + 2 * g[j]);
                 }
                 // Explicit fmaf: the rounding is the same in either batch
-                // size. A contributor adds to its own head and adds weight 0
-                // (an exact +0) to the other, so no register array is
-                // indexed at run time.
-#pragma unroll
-                for (int k = 0; k < MB; ++k) {
-                    const int e = cb + k;
-                    if (e >= nc) break;
-                    const bool inA = e < nA;
+                // size. Which head a contributor adds to is a wave-uniform
+                // branch with fixed register indices (an index chosen at run
+                // time would put the accumulators in scratch).
+                auto add = [&](floatx4(&ac)[2], float(&Lh)[2], int k) __attribute__((always_inline)) {
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        const float w = mv[k][j].x, lw = mv[k][j].y;
-                        const float wa = inA ? w : 0.0f, wb = inA ? 0.0f : w;
-                        L[0][j] += inA ? lw : 0.0f;
-                        L[1][j] += inA ? 0.0f : lw;
-                        acc[0][j][0] = __builtin_fmaf(ov[k][j].x, wa, acc[0][j][0]);
-                        acc[0][j][1] = __builtin_fmaf(ov[k][j].y, wa, acc[0][j][1]);
-                        acc[0][j][2] = __builtin_fmaf(ov[k][j].z, wa, acc[0][j][2]);
-                        acc[0][j][3] = __builtin_fmaf(ov[k][j].w, wa, acc[0][j][3]);
-                        acc[1][j][0] = __builtin_fmaf(ov[k][j].x, wb, acc[1][j][0]);
-                        acc[1][j][1] = __builtin_fmaf(ov[k][j].y, wb, acc[1][j][1]);
-                        acc[1][j][2] = __builtin_fmaf(ov[k][j].z, wb, acc[1][j][2]);
-                        acc[1][j][3] = __builtin_fmaf(ov[k][j].w, wb, acc[1][j][3]);
+                        const float w = mv[k][j].x;
+                        Lh[j] += mv[k][j].y;
+                        ac[j][0] = __builtin_fmaf(ov[k][j].x, w, ac[j][0]);
+                        ac[j][1] = __builtin_fmaf(ov[k][j].y, w, ac[j][1]);
+                        ac[j][2] = __builtin_fmaf(ov[k][j].z, w, ac[j][2]);
+                        ac[j][3] = __builtin_fmaf(ov[k][j].w, w, ac[j][3]);
                     }
-                }
+                };
+                // Head A's contributors come first in the list, B's after.
+                const int kA = min(MB, nA - cb), kn = min(MB, nc - cb);
+#pragma unroll
+                for (int k = 0; k < MB; ++k)
+                    if (k < kA) add(acc[0], L[0], k);
+#pragma unroll
+                for (int k = 0; k < MB; ++k)
+                    if (k >= kA && k < kn) add(acc[1], L[1], k);
             };
             // Most merges hold at most 8 contributors: a batch of 8 keeps
             // their loads, LDS reads and folds to what they use.
