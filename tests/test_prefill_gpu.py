@@ -120,6 +120,20 @@ def test_the_encoder_attention_off_its_rows_is_the_split_path(gpu, t, heads, sta
     assert bad == 0, f"t {t} heads {heads}: {bad} of {want.size} differ"
 
 
+@pytest.mark.parametrize("t,heads", [(1500, 20), (150, 4), (77, 3), (1, 2), (129, 1)])
+def test_the_eight_wave_encoder_is_the_four_wave_one(gpu, t, heads, monkeypatch):
+    """The encoder rows run on eight-wave workgroups of one 16-row query tile
+    per wave; each row's arithmetic is that of the four-wave kernel (two
+    tiles per wave, or one), so the f16 contexts agree bit for bit."""
+    hd = 64
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    qkv = up(oracle.seq(t * 3 * heads * hd, 612) * np.float32(3.0))
+    got = down(gpu.flash_attn_rows(qkv, t, heads, hd, scale)).view(np.uint16)
+    monkeypatch.setenv("LLMTIE_ROWS_W8", "0")
+    want = down(gpu.flash_attn_rows(qkv, t, heads, hd, scale)).view(np.uint16)
+    assert np.array_equal(got, want), f"t {t} heads {heads}: {int((got != want).sum())} differ"
+
+
 @pytest.mark.skip(reason="removed route: the encoder rows once went through a tiled f16 copy in a cached "
                          "workspace (f32_to_t16_kernel<64, false>) into flash_fwd_kernel<64, PF_T16>; one MI355X "
                          "run of it at 1500 rows x 20 heads ended in a GPU memory fault with no cause found in its "

@@ -128,7 +128,8 @@ int pick_nqt(size_t tq, size_t heads, int gb, bool staged = false) {
     if (wg2 >= 512) return 2;
     // f32 sources staged through registers: two tiles per wave halve the
     // staging per query row, which wins down to about one workgroup per CU
-    // (C4 encoder, 240 workgroups: 38.7 vs 40.1 us).
+    // (the encoder rows at 240 workgroups: 38.7 vs 40.1 us, before their
+    // eight-wave kernel).
     if (staged && wg2 >= 192) return 2;
     return 1;
 }
@@ -463,6 +464,11 @@ int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint1
     a.out_f16 = 1;
     // The stacked f32 rows are read in place: the attention kernel stages
     // them through registers into its f16 LDS tiles (no copy, no workspace).
+    // Eight-wave workgroups of one query tile per wave: the staging per row
+    // of two tiles per wave, at two waves per SIMD (C4 encoder 38.2 -> 35.8
+    // us). LLMTIE_ROWS_W8=0 selects the four-wave kernel.
+    const char* w8 = getenv("LLMTIE_ROWS_W8");
+    if (!(w8 && !atoi(w8))) return launched("flash_attn_rows", launch_prefill(64, PF_ROWS, 1, a, S(stream), 8));
     return launched("flash_attn_rows", launch_prefill(64, PF_ROWS, pick_nqt(t, heads, 1, true), a, S(stream)));
 }
 

@@ -38,7 +38,8 @@ struct PrefillArgs {
     int grid8;  // workgroups of the 1-D launch / 8 (read with the arguments, not from the dispatch packet)
 };
 
-// nqt: 16-query tiles per wave (1, 2 or 4).
-hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st);
+// nqt: 16-query tiles per wave (1, 2 or 4). waves: 4, or 8 for the encoder
+// rows at nqt 1 (otherwise ignored).
+hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st, int waves = 4);
 
 }  // namespace llmtie

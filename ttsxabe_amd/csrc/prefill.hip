@@ -403,8 +403,12 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
 // Keys past the cache's live ones: K rows are clamped to the last live row
 // (their scores are masked); V chunks past ktot may hold anything, so in the
 // one tile that reaches past ktot they are zeroed in LDS before use.
-template <int HD, int KIND, int NQT>
-__global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
+// W: waves per workgroup, 4, or 8 for the encoder rows (NQT = 1: the tile
+// staging per query row of two query tiles per wave, at two waves per SIMD).
+template <int HD, int KIND, int NQT, int W>
+__global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(PrefillArgs a) {
+    static_assert(W == PW || (W == 8 && KIND == PF_ROWS), "eight waves: encoder rows only");
+    constexpr int TW = W * LLMTIE_WAVE;
     static_assert(KIND == PF_F16 || KIND == PF_T16 || KIND == PF_F32 || KIND == PF_ROWS, "unknown source");
     // f32 sources (the f32 cache, the stacked encoder rows) are staged through
     // registers: loaded as f32, rounded to f16 and written to LDS in the same
@@ -416,8 +420,8 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     constexpr int KF = 4 * NS;          // K fragments per tile
     constexpr int VF = 2 * NT;          // V fragments per tile
     constexpr int FH = 64 * 8;          // halves per fragment
-    constexpr int NF = (KF + VF) / PW;  // fragments each wave loads per tile
-    static_assert((KF + VF) % PW == 0, "fragments split evenly over the waves");
+    constexpr int NF = (KF + VF) / W;  // fragments each wave loads per tile
+    static_assert((KF + VF) % W == 0, "fragments split evenly over the waves");
     __shared__ __attribute__((aligned(16))) half_t t0[(KF + VF) * FH];
     __shared__ __attribute__((aligned(16))) half_t t1[(KF + VF) * FH];
 
@@ -425,7 +429,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     const int lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int gb = a.gb;
-    const int pb = QPW * (PW / gb);
+    const int pb = QPW * (W / gb);
     const int group = a.heads / a.kv_heads;
     int rb = blockIdx.x, gy = blockIdx.y;
     if (a.xcd) {
@@ -451,7 +455,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     const __amdgpu_buffer_rsrc_t rv =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.v), 0, (int)(uint32_t)a.v_bytes, 0x00020000);
 
-    // Register staging (STAGED kinds). Fragment f = wave + PW * i of a tile,
+    // Register staging (STAGED kinds). Fragment f = wave + W * i of a tile,
     // lane (col, grp): K fragment (half, T, s) is key 32*half + 8*(col/4) +
     // 4T + col%4, dims 32s + 8grp .. +7 (two float4 of one K row); V fragment
     // (half, t) is dim 16t + col, keys 32*half + 8grp .. +7 (two float4 of
@@ -467,19 +471,20 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     const bool vvec = KIND == PF_F32 && a.cap % 4 == 0;  // V^T rows 16-byte aligned
     constexpr int NSR = STAGED ? NF : 1;
     float4 sr[NSR][2];
-    // Stacked rows: V is [key][dim], so a thread takes 4 dims x 4 keys
-    // (one float4 from each of 4 rows; 16 threads cover one 256-byte row
-    // segment) instead of one fragment chunk, and writes each dim's 4 keys
-    // as one 8-byte half of a chunk. The V fragments are the wave's last
-    // NF - KF / PW staging slots.
-    static_assert(KIND != PF_ROWS || (HD == 64 && KF % PW == 0 && VF * 64 * 8 == PT * 16), "rows: hd 64");
-    constexpr int KI = KF / PW;  // staging slots holding K fragments
-    const int rdq = tid & 15, rkq = tid >> 4;  // rows V: dims 4*rdq .. +3, keys 4*rkq .. +3
+    // Stacked rows: V is [key][dim], so a thread takes 4 dims x VR keys
+    // (one float4 from each of VR rows; 16 threads cover one 256-byte row
+    // segment) instead of one fragment chunk, and writes each dim's VR keys
+    // as one 2·VR-byte piece of a chunk. The V fragments are the wave's last
+    // NF - KF / W staging slots.
+    constexpr int KI = KF / W;         // staging slots holding K fragments
+    constexpr int VR = 1024 / TW;      // rows V: keys per thread (4, or 2 at eight waves)
+    static_assert(KIND != PF_ROWS || (HD == 64 && KF % W == 0 && 2 * (NF - KI) == VR), "rows: hd 64");
+    const int rdq = tid & 15, kb = VR * (tid >> 4);  // rows V: dims 4*rdq .. +3, keys kb .. kb + VR - 1
     auto stage_load = [&](int kv0) __attribute__((always_inline)) {
         if constexpr (KIND == PF_ROWS) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int key = kv0 + 4 * rkq + u;
+            for (int u = 0; u < VR; ++u) {
+                const int key = kv0 + kb + u;
                 const float4 x = *reinterpret_cast<const float4*>(vf32 + svb + (size_t)min(key, ktot - 1) * a.kvs +
                                                                   4 * rdq);
                 sr[KI + u / 2][u % 2] = key < ktot ? x : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -488,7 +493,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
         if constexpr (STAGED) {
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
-                const int f = wave + PW * i;
+                const int f = wave + W * i;
                 if (KIND == PF_ROWS && i >= KI) continue;
                 if (f < KF) {
                     const int hf = f / (2 * NS), T = (f / NS) & 1, s = f % NS;
@@ -522,28 +527,31 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     };
     auto stage_store = [&](half_t* dst) __attribute__((always_inline)) {
         if constexpr (KIND == PF_ROWS) {
-            // Dim 4*rdq + e, keys 4*rkq .. +3: V fragment (half, t) = (rkq / 8,
-            // dim / 16), lane (dim % 16) + 16 * ((rkq % 8) / 2), halves 4 * (rkq % 2) ..
-            const float4 x[4] = {sr[KI][0], sr[KI][1], sr[KI + 1][0], sr[KI + 1][1]};
+            // Dim 4*rdq + e, keys kb .. kb + VR - 1: V fragment (half, t) =
+            // (kb / 32, dim / 16), lane (dim % 16) + 16 * ((kb / 8) % 4), halves kb % 8 ..
+            typedef _Float16 hv __attribute__((ext_vector_type(VR)));
+            float4 x[VR];
+#pragma unroll
+            for (int u = 0; u < VR; ++u) x[u] = sr[KI + u / 2][u % 2];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int dd = 4 * rdq + e;
-                half4 y;
+                hv y;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) y[u] = to_h(e == 0 ? x[u].x : e == 1 ? x[u].y : e == 2 ? x[u].z : x[u].w);
-                const int frag = KF + (rkq >> 3) * NT + (dd >> 4);
+                for (int u = 0; u < VR; ++u) y[u] = to_h(e == 0 ? x[u].x : e == 1 ? x[u].y : e == 2 ? x[u].z : x[u].w);
+                const int frag = KF + (kb >> 5) * NT + (dd >> 4);
                 // Chunk (lane) index XOR the dim tile: a wave's 16 dims of one
                 // instruction land on 16 distinct 16-byte bank slots (unswizzled,
                 // the four dim tiles' chunks share 4 slots). The fragment read
                 // applies the same XOR (rows_lane).
-                const int ln = ((dd & 15) + 16 * ((rkq & 7) >> 1)) ^ (dd >> 4);
-                *reinterpret_cast<half4*>(dst + frag * FH + ln * 8 + 4 * (rkq & 1)) = y;
+                const int ln = ((dd & 15) + 16 * ((kb >> 3) & 3)) ^ (dd >> 4);
+                *reinterpret_cast<hv*>(dst + frag * FH + ln * 8 + (kb & 7)) = y;
             }
         }
         if constexpr (STAGED) {
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
-                const int f = wave + PW * i;
+                const int f = wave + W * i;
                 if (KIND == PF_ROWS && i >= KI) continue;
                 const float4 x0 = sr[i][0], x1 = sr[i][1];
                 half8 y;
@@ -557,7 +565,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     auto issue = [&](int kv0, half_t* dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
-            const int f = wave + PW * i;
+            const int f = wave + W * i;
             half_t* l = dst + f * FH;
             if constexpr (STAGED) {
                 (void)l;
@@ -740,7 +748,7 @@ __global__ __launch_bounds__(PT, 2) void flash_fwd_kernel(PrefillArgs a) {
     // Zero the V entries of keys >= ktot in a tile that reaches past ktot.
     auto zero_tail = [&](half_t* tb, int kv0) __attribute__((always_inline)) {
         half8* vf = reinterpret_cast<half8*>(tb + KF * FH);
-        for (int c = tid; c < VF * 64; c += PT) {
+        for (int c = tid; c < VF * 64; c += TW) {
             const int hf = c / (NT * 64), ln = c % 64;
             const int k0 = kv0 + 32 * hf + 8 * (ln >> 4);
             if (k0 + 8 > ktot) {
@@ -1126,9 +1134,11 @@ __global__ __launch_bounds__(PPW * LLMTIE_WAVE, 1) void flash_pp_kernel(PrefillA
     }
 }
 
-hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st) {
-    const int pb = 16 * nqt * (PW / a.gb);
-    dim3 grid((a.tq + pb - 1) / pb, a.heads / a.gb), block(PT);
+hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipStream_t st, int waves) {
+    // Eight-wave workgroups: the encoder rows at one query tile per wave only.
+    const bool w8 = waves == 8 && hd == 64 && kind == PF_ROWS && nqt == 1;
+    const int pb = 16 * nqt * ((w8 ? 8 : PW) / a.gb);
+    dim3 grid((a.tq + pb - 1) / pb, a.heads / a.gb), block(w8 ? 8 * LLMTIE_WAVE : PT);
 #define L(HD, KIND, NQ)                                                                      \
     if (hd == HD && kind == KIND && nqt == NQ) {                                             \
         hipLaunchKernelGGL((flash_prefill_kernel<HD, KIND, NQ>), grid, block, 0, st, a);     \
@@ -1144,6 +1154,7 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
     const bool f32ok = (kind == PF_F32 && al16) || (kind == PF_ROWS && al16 && a.kvs % 4 == 0);
     const bool fast = (kind == PF_T16 || (kind == PF_F16 && a.v_bytes <= 0xffffffffull) || f32ok) &&
                       (a.scale_q || a.scale > 0.0f) && !getenv("LLMTIE_PREFILL_STAGED");
+    if (w8 && !fast) return launch_prefill(hd, kind, nqt, a, st, 4);
     // Long prefills of an f16 cache: the ping-pong kernel, once its 64-row
     // workgroups still fill the chip (LLMTIE_PREFILL_PP=0 turns it off, =1
     // forces it where it applies).
@@ -1174,9 +1185,13 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
         b.xcd = items % 8 == 0 && !(getenv("LLMTIE_PREFILL_XCD") && !atoi(getenv("LLMTIE_PREFILL_XCD")));
         b.grid8 = (int)(items / 8);
         const dim3 g = b.xcd ? dim3(items) : grid;
+        if (w8) {
+            hipLaunchKernelGGL((flash_fwd_kernel<64, PF_ROWS, 1, 8>), g, block, 0, st, b);
+            return hipGetLastError();
+        }
 #define F(HD, KIND, NQ)                                                                    \
     if (hd == HD && kind == KIND && nqt == NQ) {                                           \
-        hipLaunchKernelGGL((flash_fwd_kernel<HD, KIND, NQ>), g, block, 0, st, b);          \
+        hipLaunchKernelGGL((flash_fwd_kernel<HD, KIND, NQ, PW>), g, block, 0, st, b);      \
         return hipGetLastError();                                                          \
     }
         F(64, PF_F16, 1) F(64, PF_F16, 2) F(128, PF_F16, 1) F(128, PF_F16, 2)
