@@ -98,3 +98,47 @@ def test_q8_and_tiled_sizes():
     assert L.llmtie_q8_cache_bytes(2, 8, 128, 33) == 2 * 8 * 2 * 272 * 32
     assert L.llmtie_t16_cache_len(8, 128, 4096) == 8 * 4096 * 128 * 2
     assert L.llmtie_t16_cache_len(20, 64, 1500) == 20 * 47 * 32 * 64 * 2
+
+
+W = 2**64  # size_t wraps here
+
+
+def test_extents_that_would_wrap_are_refused():
+    """Offsets and counts whose sums or products pass size_t's range must be
+    refused, not wrapped into a small value that passes the length check
+    (a wrapped q or out offset would read or write outside the buffer)."""
+    L = _lib.lib()
+    BIG = 10**9
+    # q offset and out row near the top of size_t.
+    assert L.llmtie_attn_decode_f16_q_row(NULL, NULL, BIG, W - 512, NULL, BIG, NULL, BIG, 4, 4, 128, 10, 64,
+                                          C.c_float(0.1), 0, NULL, NULL, BIG, NULL, 0, 0, 0) == 4
+    assert L.llmtie_attn_decode_f16_q_row(NULL, NULL, BIG, 0, NULL, BIG, NULL, BIG, 4, 4, 128, 10, 64,
+                                          C.c_float(0.1), 0, NULL, NULL, BIG, NULL, 0, 0, W // 512) == 4
+    # A twin whose rows * width wraps (its scales would sit at a wrapped address).
+    assert L.llmtie_attn_decode_f16_q_row(NULL, NULL, BIG, 0, NULL, BIG, NULL, BIG, 4, 4, 128, 10, 64,
+                                          C.c_float(0.1), 0, NULL, NULL, BIG, NULL, W // 512 + 1, 512, 0) == 4
+    # past + tq past the top of size_t; heads * head_dim past it.
+    assert L.llmtie_flash_attn(NULL, NULL, BIG, NULL, BIG, NULL, BIG, NULL, BIG, 1, W - 1, 4, 4, 64, 64,
+                               C.c_float(1.0), 1) == 3
+    assert L.llmtie_flash_attn(NULL, NULL, BIG, NULL, BIG, NULL, BIG, NULL, BIG, 4, 0, 2**58, 2**58, 64, 64,
+                               C.c_float(1.0), 1) == 4
+    assert L.llmtie_flash_attn_rows(NULL, NULL, BIG, NULL, BIG, 16, 2**58, 64, C.c_float(1.0)) == 4
+    # Producers: a wrapping source offset, a wrapping rope offset.
+    assert L.llmtie_cache_append(NULL, NULL, BIG, W - 8, NULL, BIG, 1, 2, 8, 16, 0, 0) == 4
+    assert L.llmtie_rope(NULL, NULL, BIG, W - 8, NULL, 1, 2, 8, C.c_float(1e4), 0) == 4
+    assert L.llmtie_kv_q8_append(NULL, NULL, BIG, W - 8, NULL, BIG, 0, NULL, BIG, 1, 0, 1, 2, 128, 64, 0) == 4
+    # Sizes that would wrap saturate.
+    assert L.llmtie_q8_cache_bytes(2**40, 2**20, 128, 64) == W - 1
+    assert L.llmtie_t16_cache_len(2**50, 128, 2**20) == W - 1
+
+
+def test_the_no_allocation_decode_refuses_before_the_device():
+    """A call beyond the fixed scratch is refused with LLMTIE_SCRATCH_LIMIT
+    before any device call, so the refusal needs no GPU."""
+    L = _lib.lib()
+    BIG = 10**12
+    P = 4096  # a placeholder address: the call is refused before anything is read or written
+    assert L.llmtie_attn_decode_f16_noalloc(NULL, P, BIG, P, BIG, P, BIG, 512, 512, 128, 4096, 4096,
+                                            C.c_float(0.1), 0, P, BIG) == 12
+    e = last()
+    assert e.field[2] > e.field[3]

@@ -71,6 +71,24 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // an overrun of the int range rather than silently wrapped.
 constexpr size_t IMAX = 0x7fffffff;
 
+// Sizes computed from caller arguments saturate at SIZE_MAX instead of
+// wrapping, so a length check on a sum or product never passes on overflow.
+size_t smul(size_t a, size_t b) {
+    size_t r;
+    return __builtin_mul_overflow(a, b, &r) ? SIZE_MAX : r;
+}
+size_t smul(size_t a, size_t b, size_t c) { return smul(smul(a, b), c); }
+size_t sadd(size_t a, size_t b) {
+    size_t r;
+    return __builtin_add_overflow(a, b, &r) ? SIZE_MAX : r;
+}
+// The first of up to four counts that does not fit an int, refused as an
+// overrun of the int range (0 when all fit).
+int over_int(size_t a, size_t b = 0, size_t c = 0, size_t d = 0) {
+    const size_t m = std::max(std::max(a, b), std::max(c, d));
+    return m > IMAX ? overrun_slice(m, IMAX) : 0;
+}
+
 }  // namespace
 
 struct llmtie_decode_scratch {
@@ -138,12 +156,14 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
                    size_t v_len, float* out, size_t out_len, size_t tq, size_t past, size_t heads, size_t kv_heads,
                    size_t hd, size_t cap, float scale, int causal) {
     if (!(hd == 64 || hd == 128) || kv_heads == 0 || heads % kv_heads != 0) return unsupported(hd, heads, kv_heads);
-    if (past + tq > cap) return overrun_cache(past + tq, cap);
-    if (heads * hd > IMAX || cap > IMAX || tq * heads * hd > (size_t)1 << 40) return overrun_slice(tq * heads * hd, IMAX);
-    if (q_len < tq * heads * hd) return overrun_slice(tq * heads * hd, q_len);
-    const size_t need = kv_heads * cap * hd;
+    if (sadd(past, tq) > cap) return overrun_cache(sadd(past, tq), cap);
+    if (int r = over_int(smul(heads, hd), cap)) return r;
+    const size_t nq = smul(tq, heads, hd);
+    if (nq > (size_t)1 << 40) return overrun_slice(nq, (size_t)1 << 40);
+    if (q_len < nq) return overrun_slice(nq, q_len);
+    const size_t need = smul(kv_heads, cap, hd);
     if (k_len < need || v_len < need) return overrun_slice(need, std::min(k_len, v_len));
-    if (out_len < tq * heads * hd) return overrun_slice(tq * heads * hd, out_len);
+    if (out_len < nq) return overrun_slice(nq, out_len);
     if (tq == 0) return ok();
     if (!q || !k || !v || !out) return invalid("a buffer");
     const size_t group = heads / kv_heads;
@@ -328,20 +348,27 @@ struct FixedScratch {
     size_t ctr_cap;   // words
 };
 
+// Sizes of the no-allocation decode's fixed scratch: split partials, then
+// arrival counters (CTR_STRIDE words per kv head).
+constexpr size_t NOALLOC_PART_FLOATS = (size_t)1 << 20;
+constexpr size_t NOALLOC_CTR_WORDS = (size_t)256 * CTR_STRIDE;
+int noalloc_scratch(hipStream_t st, FixedScratch& f);
+
 // The checks and the launch behind every single-sequence decode
 // (device.rs:6224-6410).
 int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q_off, const void* k, size_t k_len,
                   const void* v, size_t v_len, size_t heads, size_t kv_heads, size_t hd, size_t tk, size_t cap,
                   float scale, int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len,
                   size_t out_off, int8_t* twin, size_t twin_rows, size_t twin_k, bool has_twin,
-                  const FixedScratch* fixed = nullptr) {
+                  bool noalloc = false) {
     const bool tiled = kind == KV_T16;
     if (!(hd == 64 || hd == 128)) return unsupported(hd, heads, kv_heads);
     if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 16) return unsupported(hd, heads, kv_heads);
     if (tk == 0 || tk > cap) return overrun_cache(tk, cap);
     const size_t esz = kind == KV_F32 ? 4 : 2;
     if (!tiled && (cap * esz) % 8 != 0) return odd_cap(cap);
-    if (cap > IMAX || kv_heads * cap * hd > ((size_t)1 << 40)) return overrun_slice(kv_heads * cap * hd, IMAX);
+    if (int r = over_int(cap, heads)) return r;
+    if (smul(kv_heads, cap, hd) > ((size_t)1 << 40)) return overrun_slice(smul(kv_heads, cap, hd), (size_t)1 << 40);
     if (tiled) {
         const size_t need = kv_heads * (size_t)tiled_nblk((int)cap) * 64 * hd;
         if (k_len < need) return overrun_slice(need, k_len);
@@ -351,18 +378,20 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
         if (k_len < need || v_len < need) return overrun_slice(need, std::min(k_len, v_len));
     }
     const size_t n = heads * hd;
-    if (q_len < q_off + n) return overrun_slice(q_off + n, q_len);
-    if (out_len < out_off + n) return overrun_slice(out_off + n, out_len);
+    if (q_len < sadd(q_off, n)) return overrun_slice(sadd(q_off, n), q_len);
+    if (out_len < sadd(out_off, n)) return overrun_slice(sadd(out_off, n), out_len);
     if (out_off % 32 != 0) return fail(LLMTIE_RAGGED_BLOCK, out_off, 32, 0, 0, "a row of %zu in blocks of 32", out_off);
     if (has_twin) {
-        if (twin_k != n || twin_rows * twin_k < out_off + n)
+        // The scales follow the codes at twin + twin_rows * twin_k.
+        if (int r = over_int(twin_rows)) return r;
+        if (twin_k != n || smul(twin_rows, twin_k) < out_off + n)
             return fail(LLMTIE_MISMATCHED_Q8, twin_rows, twin_k, out_off / n + 1, n,
                         "an int8 twin of %zu rows by %zu where %zu by %zu is needed", twin_rows, twin_k,
                         out_off / n + 1, n);
         if (!twin) return invalid("twin");
     }
     if (!q || !k || !v || !out) return invalid("a buffer");
-    if (!scratch && !fixed) return invalid("scratch");
+    if (!scratch && !noalloc) return invalid("scratch");
     const size_t group = heads / kv_heads;
     int nit, splits;
     plan_decode(tk, kv_heads, group, nit, splits);
@@ -371,14 +400,18 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     const long ml_off = (long)(kv_heads * (size_t)splits * group * hd);
     float* part_p;
     unsigned* ctr_p;
-    if (fixed) {
-        if (part > fixed->part_cap || kv_heads * CTR_STRIDE > fixed->ctr_cap)
-            return fail(LLMTIE_SCRATCH_LIMIT, part, fixed->part_cap, kv_heads * CTR_STRIDE, fixed->ctr_cap,
+    if (noalloc) {
+        // Refused before the device is touched.
+        if (part > NOALLOC_PART_FLOATS || kv_heads * CTR_STRIDE > NOALLOC_CTR_WORDS)
+            return fail(LLMTIE_SCRATCH_LIMIT, part, NOALLOC_PART_FLOATS, kv_heads * CTR_STRIDE, NOALLOC_CTR_WORDS,
                         "the call needs %zu partial floats and %zu counter words; the fixed scratch holds %zu and "
                         "%zu",
-                        part, kv_heads * CTR_STRIDE, fixed->part_cap, fixed->ctr_cap);
-        part_p = fixed->part;
-        ctr_p = fixed->ctr;
+                        part, kv_heads * CTR_STRIDE, NOALLOC_PART_FLOATS, NOALLOC_CTR_WORDS);
+        FixedScratch f;
+        int r = noalloc_scratch(S(stream), f);
+        if (r != LLMTIE_OK) return r;
+        part_p = f.part;
+        ctr_p = f.ctr;
     } else {
         int r = ensure_scratch(scratch, part, kv_heads * CTR_STRIDE, S(stream));
         if (r != LLMTIE_OK) return r;
@@ -438,10 +471,10 @@ int llmtie_flash_attn_f16(void* stream, const float* q, size_t q_len, const uint
 int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint16_t* out, size_t out_len, size_t t,
                            size_t heads, size_t head_dim, float scale) {
     if (head_dim != 64 || heads == 0) return unsupported(head_dim, heads, heads);
+    if (int r = over_int(smul(heads, head_dim, 3), t)) return r;
     const size_t d = heads * head_dim;
-    if (d * 3 > IMAX || t > IMAX) return overrun_slice(t * 3 * d, IMAX);
-    if (qkv_len < t * 3 * d) return overrun_slice(t * 3 * d, qkv_len);
-    if (out_len < t * d) return overrun_slice(t * d, out_len);
+    if (qkv_len < smul(t, 3 * d)) return overrun_slice(smul(t, 3 * d), qkv_len);
+    if (out_len < smul(t, d)) return overrun_slice(smul(t, d), out_len);
     if (t == 0) return ok();
     if (!qkv || !out) return invalid("a buffer");
     PrefillArgs a{};
@@ -491,8 +524,6 @@ int llmtie_attn_decode_f16(void* stream, const float* q, size_t q_len, const uin
 // (a host-side stand-in, not a device address) to the device: it uses the
 // address hipGetSymbolAddress gives for the current device, obtained once per
 // device.
-constexpr size_t NOALLOC_PART_FLOATS = (size_t)1 << 20;
-constexpr size_t NOALLOC_CTR_WORDS = (size_t)256 * CTR_STRIDE;
 static __device__ __align__(256) float scratch[NOALLOC_PART_FLOATS + NOALLOC_CTR_WORDS];
 
 namespace {
@@ -530,19 +561,16 @@ extern "C" {
 int llmtie_attn_decode_f16_noalloc(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
                                    const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads, size_t head_dim,
                                    size_t tk, size_t cap, float scale, int scale_q, float* out, size_t out_len) {
-    FixedScratch f;
-    int r = noalloc_scratch(S(stream), f);
-    if (r != LLMTIE_OK) return r;
     return decode_common(stream, KV_F16, q, q_len, 0, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap, scale,
-                         scale_q, nullptr, out, out_len, 0, nullptr, 0, 0, false, &f);
+                         scale_q, nullptr, out, out_len, 0, nullptr, 0, 0, false, true);
 }
 
 int llmtie_attn_decode_f16_q(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
                              const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads, size_t head_dim,
                              size_t tk, size_t cap, float scale, int scale_q, llmtie_decode_scratch* scratch,
                              float* out, size_t out_len, int8_t* twin, size_t twin_len) {
-    const size_t n = heads * head_dim;
-    if (twin_len < n + (n / 32) * 4) return overrun_slice(n + (n / 32) * 4, twin_len);
+    const size_t n = smul(heads, head_dim);
+    if (twin_len < sadd(n, (n / 32) * 4)) return overrun_slice(sadd(n, (n / 32) * 4), twin_len);
     if (n % 32 != 0) return fail(LLMTIE_RAGGED_BLOCK, n, 32, 0, 0, "a row of %zu in blocks of 32", n);
     return decode_common(stream, KV_F16, q, q_len, 0, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap, scale,
                          scale_q, scratch, out, out_len, 0, twin, 1, n, true);
@@ -554,7 +582,7 @@ int llmtie_attn_decode_f16_q_row(void* stream, const float* q, size_t q_len, siz
                                  llmtie_decode_scratch* scratch, float* out, size_t out_len, int8_t* twin,
                                  size_t twin_rows, size_t twin_k, size_t row) {
     return decode_common(stream, KV_F16, q, q_len, q_off, k, k_len, v, v_len, heads, kv_heads, head_dim, tk, cap,
-                         scale, scale_q, scratch, out, out_len, row * heads * head_dim, twin, twin_rows, twin_k,
+                         scale, scale_q, scratch, out, out_len, smul(row, heads, head_dim), twin, twin_rows, twin_k,
                          true);
 }
 
@@ -573,7 +601,8 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     if (!(head_dim == 64 || head_dim == 128)) return unsupported(head_dim, heads, kv_heads);
     if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 16) return unsupported(head_dim, heads, kv_heads);
     if (max_tk == 0 || max_tk > cap) return overrun_cache(max_tk, cap);
-    if (cap > IMAX || nseq > 65535 || slots > IMAX) return overrun_slice(nseq, 65535);
+    if (nseq > 65535) return overrun_slice(nseq, 65535);
+    if (int r = over_int(cap, slots, heads)) return r;
     const size_t need = llmtie_q8_cache_bytes(slots, kv_heads, head_dim, cap);
     if (cache_len < need) return overrun_slice(need, cache_len);
     const size_t n = heads * head_dim;
@@ -633,9 +662,11 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
 
 int llmtie_rope(void* stream, float* x, size_t x_len, size_t off, const float* freq_div, size_t t, size_t heads,
                 size_t head_dim, float theta, size_t first) {
-    if (off + t * heads * head_dim > x_len) return overrun_slice(off + t * heads * head_dim, x_len);
+    if (int r = over_int(t, heads, head_dim, first)) return r;
+    const size_t nx = smul(t, heads, head_dim);
+    if (sadd(off, nx) > x_len) return overrun_slice(sadd(off, nx), x_len);
     if (head_dim % 2 != 0) return fail(LLMTIE_ODD_HEAD_DIM, head_dim, 0, 0, 0, "a rotary head of odd width %zu", head_dim);
-    if (t * heads * head_dim == 0) return ok();
+    if (nx == 0) return ok();
     if (!x) return invalid("x");
     return launched("rope", launch_rope(x, (long)off, freq_div, (int)t, (int)heads, (int)head_dim, theta, (int)first,
                                         S(stream)));
@@ -643,11 +674,12 @@ int llmtie_rope(void* stream, float* x, size_t x_len, size_t off, const float* f
 
 static int append_common(void* stream, const float* src, size_t src_len, size_t src_off, void* dst, size_t dst_len,
                          int f16, size_t n, size_t kv, size_t hd, size_t cap, size_t past, int tr) {
-    if (past + n > cap) return overrun_cache(past + n, cap);
+    if (sadd(past, n) > cap) return overrun_cache(sadd(past, n), cap);
     if (f16 && cap % 2 != 0) return odd_cap(cap);
-    const size_t total = n * kv * hd;
-    if (src_off + total > src_len) return overrun_slice(src_off + total, src_len);
-    if (kv * cap * hd > dst_len) return overrun_slice(kv * cap * hd, dst_len);
+    if (int r = over_int(cap, kv, hd)) return r;
+    const size_t total = smul(n, kv, hd);
+    if (sadd(src_off, total) > src_len) return overrun_slice(sadd(src_off, total), src_len);
+    if (smul(kv, cap, hd) > dst_len) return overrun_slice(smul(kv, cap, hd), dst_len);
     if (total == 0) return ok();
     if (!src || !dst) return invalid("a buffer");
     return launched("cache_append", launch_append(src, (long)src_off, dst, f16, tr, (int)n, (int)kv, (int)hd,
@@ -669,13 +701,14 @@ int llmtie_rope_cache_f16(void* stream, float* q, size_t q_len, size_t q_off, co
                           size_t k_off, const float* v, size_t v_len, size_t v_off, const float* freq_div,
                           size_t heads, size_t kv_heads, size_t head_dim, float theta, size_t pos, uint16_t* kc,
                           uint16_t* vc, size_t cache_len, size_t cap) {
-    if (pos >= cap) return overrun_cache(pos + 1, cap);
+    if (pos >= cap) return overrun_cache(sadd(pos, 1), cap);
     if (cap % 2 != 0) return odd_cap(cap);
     if (head_dim % 2 != 0) return fail(LLMTIE_ODD_HEAD_DIM, head_dim, 0, 0, 0, "a rotary head of odd width %zu", head_dim);
-    if (q_off + heads * head_dim > q_len) return overrun_slice(q_off + heads * head_dim, q_len);
-    if (k_off + kv_heads * head_dim > k_len) return overrun_slice(k_off + kv_heads * head_dim, k_len);
-    if (v_off + kv_heads * head_dim > v_len) return overrun_slice(v_off + kv_heads * head_dim, v_len);
-    if (cache_len < cap * kv_heads * head_dim) return overrun_slice(cap * kv_heads * head_dim, cache_len);
+    if (int r2 = over_int(cap, heads, head_dim)) return r2;
+    if (sadd(q_off, heads * head_dim) > q_len) return overrun_slice(sadd(q_off, heads * head_dim), q_len);
+    if (sadd(k_off, kv_heads * head_dim) > k_len) return overrun_slice(sadd(k_off, kv_heads * head_dim), k_len);
+    if (sadd(v_off, kv_heads * head_dim) > v_len) return overrun_slice(sadd(v_off, kv_heads * head_dim), v_len);
+    if (cache_len < smul(cap, kv_heads, head_dim)) return overrun_slice(smul(cap, kv_heads, head_dim), cache_len);
     if (!q || !k || !v || !kc || !vc) return invalid("a buffer");
     return launched("rope_cache_f16",
                     launch_rope_cache_f16(q, (long)q_off, k, (long)k_off, v, (long)v_off, freq_div, (int)heads,
@@ -697,8 +730,9 @@ static int grow_common(void* stream, const void* src, size_t src_len, void* dst,
         ss = cap;
         ds = new_cap;
     }
-    if (rows * ss > src_len) return overrun_slice(rows * ss, src_len);
-    if (rows * ds > dst_len) return overrun_slice(rows * ds, dst_len);
+    if (int r = over_int(rows, ss, ds)) return r;
+    if (smul(rows, ss) > src_len) return overrun_slice(smul(rows, ss), src_len);
+    if (smul(rows, ds) > dst_len) return overrun_slice(smul(rows, ds), dst_len);
     if (rows * len == 0) return ok();
     if (!src || !dst) return invalid("a buffer");
     return launched("cache_grow", launch_grow(src, dst, esz, (int)rows, (int)len, (int)ss, (int)ds, S(stream)));
@@ -718,18 +752,21 @@ int llmtie_cache_grow_f16(void* stream, const uint16_t* src, size_t src_len, uin
 static int q8_cache_checks(size_t hd, size_t heads, size_t kv, size_t cap, size_t slots, size_t slot,
                            size_t cache_len) {
     if (!(hd == 64 || hd == 128)) return unsupported(hd, heads, kv);
-    if (slot >= slots) return overrun_slice(slot + 1, slots);
+    if (slot >= slots) return overrun_slice(sadd(slot, 1), slots);
+    if (int r = over_int(cap, slots, kv)) return r;
     const size_t need = llmtie_q8_cache_bytes(slots, kv, hd, cap);
     if (cache_len < need) return overrun_slice(need, cache_len);
     return LLMTIE_OK;
 }
 
 size_t llmtie_q8_cache_bytes(size_t slots, size_t kv_heads, size_t head_dim, size_t cap) {
-    return slots * kv_heads * (size_t)tiled_nblk((int)cap) * (size_t)tq8_block_bytes((int)head_dim);
+    if (cap > IMAX) return SIZE_MAX;
+    return smul(smul(slots, kv_heads), (size_t)tiled_nblk((int)cap), (size_t)tq8_block_bytes((int)head_dim));
 }
 
 size_t llmtie_t16_cache_len(size_t kv_heads, size_t head_dim, size_t cap) {
-    return kv_heads * (size_t)tiled_nblk((int)cap) * 64 * head_dim;
+    if (cap > IMAX) return SIZE_MAX;
+    return smul(smul(kv_heads, (size_t)tiled_nblk((int)cap)), 64, head_dim);
 }
 
 int llmtie_kv_q8_append(void* stream, const float* k, size_t k_len, size_t k_off, const float* v, size_t v_len,
@@ -737,10 +774,10 @@ int llmtie_kv_q8_append(void* stream, const float* k, size_t k_len, size_t k_off
                         size_t kv_heads, size_t head_dim, size_t cap, size_t past) {
     int r = q8_cache_checks(head_dim, kv_heads, kv_heads, cap, slots, slot, cache_len);
     if (r != LLMTIE_OK) return r;
-    if (past + n > cap) return overrun_cache(past + n, cap);
-    const size_t total = n * kv_heads * head_dim;
-    if (k_off + total > k_len) return overrun_slice(k_off + total, k_len);
-    if (v_off + total > v_len) return overrun_slice(v_off + total, v_len);
+    if (sadd(past, n) > cap) return overrun_cache(sadd(past, n), cap);
+    const size_t total = smul(n, kv_heads, head_dim);
+    if (sadd(k_off, total) > k_len) return overrun_slice(sadd(k_off, total), k_len);
+    if (sadd(v_off, total) > v_len) return overrun_slice(sadd(v_off, total), v_len);
     if (total == 0) return ok();
     if (!k || !v || !cache) return invalid("a buffer");
     return launched("kv_q8_append", launch_append_q8(k, (long)k_off, v, (long)v_off, reinterpret_cast<char*>(cache),
@@ -754,10 +791,11 @@ int llmtie_rope_cache_q8(void* stream, float* q, size_t q_len, size_t q_off, con
                          size_t cache_len, size_t slots, size_t slot, size_t cap) {
     int r = q8_cache_checks(head_dim, heads, kv_heads, cap, slots, slot, cache_len);
     if (r != LLMTIE_OK) return r;
-    if (pos >= cap) return overrun_cache(pos + 1, cap);
-    if (q_off + heads * head_dim > q_len) return overrun_slice(q_off + heads * head_dim, q_len);
-    if (k_off + kv_heads * head_dim > k_len) return overrun_slice(k_off + kv_heads * head_dim, k_len);
-    if (v_off + kv_heads * head_dim > v_len) return overrun_slice(v_off + kv_heads * head_dim, v_len);
+    if (pos >= cap) return overrun_cache(sadd(pos, 1), cap);
+    if (int r2 = over_int(cap, heads, head_dim)) return r2;
+    if (sadd(q_off, heads * head_dim) > q_len) return overrun_slice(sadd(q_off, heads * head_dim), q_len);
+    if (sadd(k_off, kv_heads * head_dim) > k_len) return overrun_slice(sadd(k_off, kv_heads * head_dim), k_len);
+    if (sadd(v_off, kv_heads * head_dim) > v_len) return overrun_slice(sadd(v_off, kv_heads * head_dim), v_len);
     if (!q || !k || !v || !cache) return invalid("a buffer");
     return launched("rope_cache_q8", launch_rope_cache_q8(q, (long)q_off, k, (long)k_off, v, (long)v_off, freq_div,
                                                           (int)heads, (int)kv_heads, (int)head_dim, theta, (int)pos,
@@ -769,7 +807,7 @@ int llmtie_rope_cache_q8(void* stream, float* q, size_t q_len, size_t q_off, con
 
 static int t16_checks(size_t hd, size_t heads, size_t kv, size_t cap, size_t cache_len) {
     if (!(hd == 64 || hd == 128) || kv == 0) return unsupported(hd, heads, kv);
-    if (cap > IMAX) return overrun_slice(cap, IMAX);
+    if (int r = over_int(cap, heads, kv)) return r;
     const size_t need = llmtie_t16_cache_len(kv, hd, cap);
     if (cache_len < need) return overrun_slice(need, cache_len);
     return LLMTIE_OK;
@@ -780,9 +818,9 @@ int llmtie_t16_append(void* stream, const float* src, size_t src_len, size_t src
                       int value) {
     int r = t16_checks(head_dim, kv_heads, kv_heads, cap, cache_len);
     if (r != LLMTIE_OK) return r;
-    if (past + n > cap) return overrun_cache(past + n, cap);
-    const size_t total = n * kv_heads * head_dim;
-    if (src_off + total > src_len) return overrun_slice(src_off + total, src_len);
+    if (sadd(past, n) > cap) return overrun_cache(sadd(past, n), cap);
+    const size_t total = smul(n, kv_heads, head_dim);
+    if (sadd(src_off, total) > src_len) return overrun_slice(sadd(src_off, total), src_len);
     if (total == 0) return ok();
     if (!src || !cache) return invalid("a buffer");
     return launched("t16_append", launch_append_t16(src, (long)src_off, cache, (int)n, (int)kv_heads, (int)head_dim,
@@ -795,10 +833,11 @@ int llmtie_t16_rope_cache(void* stream, float* q, size_t q_len, size_t q_off, co
                           size_t cache_len, size_t cap) {
     int r = t16_checks(head_dim, heads, kv_heads, cap, cache_len);
     if (r != LLMTIE_OK) return r;
-    if (pos >= cap) return overrun_cache(pos + 1, cap);
-    if (q_off + heads * head_dim > q_len) return overrun_slice(q_off + heads * head_dim, q_len);
-    if (k_off + kv_heads * head_dim > k_len) return overrun_slice(k_off + kv_heads * head_dim, k_len);
-    if (v_off + kv_heads * head_dim > v_len) return overrun_slice(v_off + kv_heads * head_dim, v_len);
+    if (pos >= cap) return overrun_cache(sadd(pos, 1), cap);
+    if (int r2 = over_int(cap, heads, head_dim)) return r2;
+    if (sadd(q_off, heads * head_dim) > q_len) return overrun_slice(sadd(q_off, heads * head_dim), q_len);
+    if (sadd(k_off, kv_heads * head_dim) > k_len) return overrun_slice(sadd(k_off, kv_heads * head_dim), k_len);
+    if (sadd(v_off, kv_heads * head_dim) > v_len) return overrun_slice(sadd(v_off, kv_heads * head_dim), v_len);
     if (!q || !k || !v || !cache) return invalid("a buffer");
     return launched("t16_rope_cache",
                     launch_rope_cache_t16(q, (long)q_off, k, (long)k_off, v, (long)v_off, freq_div, (int)heads,
@@ -826,7 +865,7 @@ int llmtie_t16_from_ref(void* stream, const uint16_t* k, size_t k_len, const uin
     int r = t16_checks(head_dim, kv_heads, kv_heads, cap, cache_len);
     if (r != LLMTIE_OK) return r;
     if (live > cap) return overrun_cache(live, cap);
-    const size_t need = kv_heads * cap * head_dim;
+    const size_t need = smul(kv_heads, cap, head_dim);
     if (k_len < need || v_len < need) return overrun_slice(need, std::min(k_len, v_len));
     if (live == 0) return ok();
     if (!k || !v || !cache) return invalid("a buffer");
@@ -846,7 +885,7 @@ int llmtie_attn_decode_t16_q_row(void* stream, const float* q, size_t q_len, siz
                                  size_t cap, float scale, int scale_q, llmtie_decode_scratch* scratch, float* out,
                                  size_t out_len, int8_t* twin, size_t twin_rows, size_t twin_k, size_t row) {
     return decode_common(stream, KV_T16, q, q_len, q_off, cache, cache_len, nullptr, 0, heads, kv_heads, head_dim,
-                         tk, cap, scale, scale_q, scratch, out, out_len, row * heads * head_dim, twin, twin_rows,
+                         tk, cap, scale, scale_q, scratch, out, out_len, smul(row, heads, head_dim), twin, twin_rows,
                          twin_k, twin != nullptr);
 }
 
@@ -857,7 +896,7 @@ int llmtie_flash_attn_t16(void* stream, const float* q, size_t q_len, const uint
     if (r != LLMTIE_OK) return r;
     // The tiled cache holds both areas in one buffer; the length checks of the
     // shared path are satisfied by passing the whole-cache extent for both.
-    const size_t ext = kv_heads * cap * head_dim;
+    const size_t ext = smul(kv_heads, cap, head_dim);
     return prefill_common(stream, PF_T16, q, q_len, cache, ext, cache, ext, out, out_len, tq, past, heads, kv_heads,
                           head_dim, cap, scale, causal);
 }
