@@ -653,16 +653,21 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-            for (int T = 0; T < 2; ++T) {
+            for (int T = 0; T < 2; ++T)
 #pragma unroll
                 for (int u = 0; u < NQT; ++u) sc[hf][T][u] = zero_f4();
+        // Dims outermost: 4 * NQT independent accumulators between two
+        // products into the same one (each still sums its dims in order).
 #pragma unroll
-                for (int s = 0; s < NS; ++s) {
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int T = 0; T < 2; ++T) {
                     const half8 af = kf[((hf * 2 + T) * NS + s) * 64 + lane];
 #pragma unroll
                     for (int u = 0; u < NQT; ++u) sc[hf][T][u] = mfma16(af, qb[u][s], sc[hf][T][u]);
                 }
-            }
         // Software pipeline: PD fragment reads ahead of the MFMAs using them.
         {
             constexpr int NR = 4 * NS, PD = LLMTIE_PF_PD < NR ? LLMTIE_PF_PD : NR;
@@ -983,16 +988,21 @@ __global__ __launch_bounds__(PPW * LLMTIE_WAVE, 1) void flash_pp_kernel(PrefillA
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-            for (int T = 0; T < 2; ++T) {
+            for (int T = 0; T < 2; ++T)
 #pragma unroll
                 for (int u = 0; u < NQT; ++u) sc[hf][T][u] = zero_f4();
+        // Dims outermost: 4 * NQT independent accumulators between two
+        // products into the same one (each still sums its dims in order).
 #pragma unroll
-                for (int s = 0; s < NS; ++s) {
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int T = 0; T < 2; ++T) {
                     const half8 af = kf[((hf * 2 + T) * NS + s) * 64 + lane];
 #pragma unroll
                     for (int u = 0; u < NQT; ++u) sc[hf][T][u] = mfma16(af, qb[u][s], sc[hf][T][u]);
                 }
-            }
         {
             constexpr int NR = 4 * NS, PD = LLMTIE_PF_PD < NR ? LLMTIE_PF_PD : NR;
             __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
