@@ -174,3 +174,31 @@ def test_the_ping_pong_prefill_is_the_single_group_one(gpu, heads, kv, hd, causa
     got = down(run())
     assert np.isfinite(got).all()
     assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
+
+
+def test_the_long_prefill_at_its_full_shape(gpu, monkeypatch):
+    """C3's shape at 8192 rows (32/8/128, causal, tiled cache), the size the
+    ping-pong kernel runs at: sampled rows against the reference's f64
+    prefill (row r of a causal prefill is the one-row prefill at past = r,
+    so the oracle's cost is one row's, kernels.rs:2290-2374 and its rule),
+    and the whole output bit-identical to the four-wave kernel's."""
+    from ttsxabe_amd.gpu import TiledCache16
+    heads, kv, hd, tq = 32, 8, 128, 8192
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    q = oracle.seq(tq * heads * hd, 71) * np.float32(100.0)
+    kc, vc = caches(oracle.seq(kv * tq * hd, 72), oracle.seq(kv * tq * hd, 73), kv, tq, tq, hd)
+    t = TiledCache16(kv, hd, tq, zero=False)
+    gpu.t16_from_ref(up_f16(kc), up_f16(vc), t, tq)
+    dq = up(q)
+    got = down(gpu.flash_attn_t16(dq, t, tq, 0, heads, scale, True)).astype(np.float64)
+    monkeypatch.setenv("LLMTIE_PREFILL_PP", "0")
+    four = down(gpu.flash_attn_t16(dq, t, tq, 0, heads, scale, True)).astype(np.float64)
+    assert np.array_equal(got, four), "the ping-pong kernel differs from the four-wave one at 8192 rows"
+    n = heads * hd
+    rows = [0, 1, 31, 32, 63, 64, 2047, 4096, 6001, 8191]
+    for r in rows:
+        want, spread = oracle.prefill_ref(q[r * n:(r + 1) * n], n, kc, vc, 1, r, heads, kv, hd, tq, scale, True)
+        tol = 2e-4 + 1e-2 * np.abs(want) + 1e-2 * spread
+        err = np.abs(want - got[r * n:(r + 1) * n])
+        worst = float((err / tol).max())
+        assert worst < 0.5, f"row {r}: worst error {worst} of its tolerance"
