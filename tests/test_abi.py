@@ -142,3 +142,22 @@ def test_the_no_allocation_decode_refuses_before_the_device():
                                             C.c_float(0.1), 0, P, BIG) == 12
     e = last()
     assert e.field[2] > e.field[3]
+
+
+def test_the_batched_q8_decode_refuses_groups_over_its_lds_budget():
+    """The stream-K kernel keeps one tiled block per wave plus two query
+    buffers of group * head_dim floats per wave in LDS; groups whose buffers
+    would pass a workgroup's 160 KB are refused before any device call (16
+    is the largest at head_dim 64 and 128), as are caches whose one (slot,
+    kv head) run of blocks passes the kernel's 32-bit buffer range."""
+    L = _lib.lib()
+    BIG = 10**12
+    P = 4096
+    for hd in (64, 128):
+        assert L.llmtie_attn_decode_q8_batch(NULL, P, BIG, P, BIG, 1, P, P, 1, 64, 17 * 2, 2, hd, 64,
+                                             C.c_float(0.1), 0, P, P, BIG) == 1
+        assert list(last().field)[:3] == [hd, 34, 2]
+    # (2**31 / 8704) blocks of 32 positions at head_dim 128 is the range's limit.
+    cap = (2**31 // 8704 + 1) * 32
+    assert L.llmtie_attn_decode_q8_batch(NULL, P, BIG, P, BIG, 1, P, P, 1, 64, 32, 8, 128, cap,
+                                         C.c_float(0.1), 0, P, P, BIG) == 3

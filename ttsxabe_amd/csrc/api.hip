@@ -599,9 +599,15 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
                                 float scale, int scale_q, llmtie_decode_scratch* scratch, float* out,
                                 size_t out_len) {
     if (!(head_dim == 64 || head_dim == 128)) return unsupported(head_dim, heads, kv_heads);
-    if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 16) return unsupported(head_dim, heads, kv_heads);
+    // Groups are bounded by the stream-K kernel's LDS (sk_group_max: 16 at
+    // head_dim 64 and 128).
+    if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > (size_t)sk_group_max((int)head_dim))
+        return unsupported(head_dim, heads, kv_heads);
     if (max_tk == 0 || max_tk > cap) return overrun_cache(max_tk, cap);
     if (nseq > 65535) return overrun_slice(nseq, 65535);
+    // The stream-K kernel addresses one (slot, kv head)'s blocks through a
+    // 32-bit buffer range.
+    if (smul((cap + 31) / 32, sk_block_bytes((int)head_dim)) > 0x7fffffffu) return overrun_cache(cap, 0x7fffffffu / sk_block_bytes((int)head_dim) * 32);
     if (int r = over_int(cap, slots, heads)) return r;
     const size_t need = llmtie_q8_cache_bytes(slots, kv_heads, head_dim, cap);
     if (cache_len < need) return overrun_slice(need, cache_len);
@@ -623,7 +629,7 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     size_t part = nseq * kv_heads * ((size_t)splits * group * head_dim + mls);
     long ml_off = (long)(nseq * kv_heads * (size_t)splits * group * head_dim);
     if (sk) {
-        const size_t slots2 = (size_t)items * 4 * 2;
+        const size_t slots2 = (size_t)items * SK_WAVES * 2;
         ml_off = (long)(slots2 * 16 * head_dim);
         part = slots2 * (16 * head_dim + 32);
     }

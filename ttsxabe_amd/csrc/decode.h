@@ -65,6 +65,25 @@ struct DecodeArgs {
     int grid8;
 };
 
+// LDS of the stream-K batched Q8_0 kernel (four waves, each with one ring
+// slot of a whole tiled block and two raw query buffers of group * hd
+// floats), against the 160 KB a gfx950 workgroup can hold. The kernel
+// static_asserts its ring plus the largest query buffers fits; the entry
+// point refuses any group whose buffers would not (sk_group_max).
+constexpr size_t SK_LDS_MAX = 160 * 1024;
+constexpr int SK_WAVES = 4;
+constexpr size_t sk_block_bytes(int hd) { return 2 * 32 * (size_t)hd + 2 * 32 * (size_t)(hd / 32) * 2; }
+constexpr size_t sk_qdyn_bytes(int hd, int group) { return (size_t)SK_WAVES * 2 * group * hd * sizeof(float); }
+constexpr size_t sk_lds_bytes(int hd, int group) { return SK_WAVES * sk_block_bytes(hd) + sk_qdyn_bytes(hd, group); }
+constexpr size_t sk_qdyn_max(int hd) { return sk_qdyn_bytes(hd, 16); }
+// The largest GQA group whose stream-K launch fits the LDS (16 at hd 64 and 128).
+constexpr int sk_group_max(int hd) {
+    int g = 16;
+    while (g > 0 && sk_lds_bytes(hd, g) > SK_LDS_MAX) --g;
+    return g;
+}
+static_assert(sk_group_max(64) == 16 && sk_group_max(128) == 16, "stream-K groups up to 16 fit the LDS");
+
 hipError_t launch_decode(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st);
 
 // Fills n words with v (a kernel, so it may sit inside a captured graph).

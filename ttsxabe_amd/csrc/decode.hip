@@ -414,6 +414,109 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
     }
 }
 
+// One tiled Q8_0 block folded into the wave's running softmax state: the
+// arithmetic of fold_block<HD, KV_TQ8>, bit for bit, in an order that keeps
+// the matrix unit and the VALU busy together (one wave per SIMD issues a
+// VALU instruction only every ~6-7 clocks, so the stream-K kernel's blocks
+// cost their VALU count). Every K fragment is dequantised first; the sixteen
+// score MFMAs (hi halves of the queries, then lo, so no MFMA waits on the one
+// before it) run while the V fragments are dequantised; the scaled scores,
+// the softmax and P' follow, and the value MFMAs close the block.
+// (Codes entering the MFMAs biased, 1152 + code, with the bias cancelled in
+// the accumulator: for V no loss and no gain; for K the score accumulators
+// lost precision to 1.07e-3 of full scale on 8-key sequences, not kept.)
+template <int HD, bool MASK>
+__device__ __forceinline__ void fold_block_q8(const Frag<HD, KV_TQ8>& f, const half8 (&qh)[HD / 32],
+                                              const half8 (&ql)[HD / 32], int p0, int tk, int grp,
+                                              float& m_run, float& l_run, floatx4 (&o)[HD / 16]) {
+    constexpr int NS = HD / 32;
+    constexpr int NT = HD / 16;
+    half8 kq[2][NS];
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const uint4& w = f.kc[T][s >> 1];
+            kq[T][s] = (s & 1) ? dq8(w.z, w.w) : dq8(w.x, w.y);
+        }
+    floatx4 b[2][NS];
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int s = 0; s < NS; ++s) b[T][s] = mfma16(kq[T][s], qh[s], zero_f4());
+    half8 vq[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const uint4& w = f.vc[t >> 1];
+        vq[t] = (t & 1) ? dq8(w.z, w.w) : dq8(w.x, w.y);
+    }
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int s = 0; s < NS; ++s) b[T][s] = mfma16(kq[T][s], ql[s], b[T][s]);
+    float sc[8];
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+        floatx4 acc = zero_f4();
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += (float)h_at(f.ks[s], 4 * T + r) * b[T][s][r];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[4 * T + r] = acc[r];
+    }
+    const int kb = p0 + 8 * grp;
+    float mx = ninf();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sc[j] = (!MASK || kb + j < tk) ? sc[j] : ninf();
+        mx = fmaxf(mx, sc[j]);
+    }
+    mx = max4grp(mx);
+    const float mn = fmaxf(m_run, mx);
+    const float fac = ex2(m_run - mn);
+    m_run = mn;
+    // Probabilities carry a factor 2^10 (see fold_block).
+    const float mb = mn - 10.0f;
+    float p[8], ps = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        p[j] = ex2(sc[j] - mb);
+        ps += p[j];
+    }
+    l_run = l_run * fac + ps;
+    if (__any(fac != 1.0f)) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) o[t] *= fac;
+    }
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 ph[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a0 = (!MASK || kb + 2 * i < tk) ? p[2 * i] : 0.0f;
+        const float a1 = (!MASK || kb + 2 * i + 1 < tk) ? p[2 * i + 1] : 0.0f;
+        ph[i] = h2{to_h(a0), to_h(a1)};
+    }
+#pragma unroll
+    for (int bb = 0; bb < NS; ++bb) {
+        const uint32_t dw[4] = {f.vs[bb].x, f.vs[bb].y, f.vs[bb].z, f.vs[bb].w};
+        half8 pv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h2 d = __builtin_bit_cast(h2, dw[i]);
+            if constexpr (MASK) {
+                if (kb + 2 * i >= tk) d[0] = (half_t)0.0f;
+                if (kb + 2 * i + 1 >= tk) d[1] = (half_t)0.0f;
+            }
+            const h2 x = ph[i] * d;
+            pv[2 * i] = x[0];
+            pv[2 * i + 1] = x[1];
+        }
+#pragma unroll
+        for (int t = 2 * bb; t < 2 * bb + 2; ++t) o[t] = mfma16(vq[t], pv, o[t]);
+    }
+}
+
 // One element of the context, and its int8 twin: the 32 threads of a scale
 // group are 32 consecutive lanes of one wave (the caller guarantees it).
 __device__ __forceinline__ void emit(float* out, int8_t* tc, float* ts, size_t idx, float y) {
@@ -1272,15 +1375,19 @@ __device__ __forceinline__ void q_read<64>(uint32_t b, float4 (&x)[2][2]) {
         : "v"(b));
 }
 
-// The Q8_0 stream-K kernel. Each wave owns a two-slot ring of whole tiled
-// blocks in LDS, filled by direct-to-LDS loads (no registers held while a
-// block is in flight): fold i waits for slot i % 2, reads the block into
-// registers, refills the slot with block i + 2 and folds from registers, so
-// two blocks are always on their way. One workgroup per compute unit: at
-// two, 2048 concurrent streams measured slower (first data up to 17 us late,
-// and 256 VGPRs spill).
+// The Q8_0 stream-K kernel. Each wave owns one LDS slot of a whole tiled
+// block, filled by direct-to-LDS loads (no registers held while a block is
+// in flight): fold i waits for the slot, reads block i into registers,
+// refills the slot with block i + 1 and folds from registers. The wave is
+// busy most of a block's period (the loads' issue, the LDS read and the
+// fold), so a deeper ring only adds bytes in flight, and more bytes in flight
+// than one block per wave measured slower (two-slot ring 58.9 vs 58.6 us,
+// three-slot slower again). One workgroup per compute unit: at two, 2048
+// concurrent streams measured slower (first data up to 17 us late).
 template <int HD>
 __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
+    constexpr int W = DW;
+    constexpr int RING = 1;
     constexpr int KIND = KV_TQ8;
     constexpr int NS = HD / 32;
     constexpr int NT = HD / 16;
@@ -1289,13 +1396,17 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     constexpr int SCL_L = (BB - 64 * HD) / 16;    // lanes of the one scale load
     constexpr int LPB = CODE_I + 1;               // load instructions per block
     static_assert(SCL_L <= 64, "scales in one wave-wide load");
-    __shared__ __attribute__((aligned(16))) char ring[DW][2][BB];
+    __shared__ __attribute__((aligned(16))) char ring[W][RING][BB];
+    // The LDS budget: the ring plus the largest query buffers the host
+    // launches with (two of group <= 16 rows of HD floats per wave).
+    static_assert(W == SK_WAVES && BB == (int)sk_block_bytes(HD), "the host's LDS arithmetic");
+    static_assert(sizeof(ring) + sk_qdyn_max(HD) <= SK_LDS_MAX, "stream-K LDS over a workgroup's 160 KB");
     // Dynamic: per wave, one raw query buffer of group * HD floats (the
     // destination of a segment's direct-to-LDS query loads).
     extern __shared__ __attribute__((aligned(16))) float sk_qraw[];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
     const int group = a.group, kv = a.kv_heads;
     const int n = group * HD;           // context floats per (sequence, kv head)
@@ -1303,8 +1414,8 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
 
     const SkSeqs sq = sk_seqs(a, lane);
     const long total = sq.total;
-    const long nw = min((long)a.items * DW, total);
-    const long u = (long)blockIdx.x * DW + wave;
+    const long nw = min((long)a.items * W, total);
+    const long u = (long)blockIdx.x * W + wave;
 
     // A sequence the batch describes wrongly gets a NaN row (written by the
     // launch's first wave), never a read outside its cache.
@@ -1352,7 +1463,7 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     // retire in issue order on this part), and the count just after each
     // ring slot's block: a fold waits with vmcnt = everything issued since.
     // Every instruction counted here is issued with lane 0 active.
-    int vm_ops = 0, mark[2] = {0, 0};
+    int vm_ops = 0, mark[RING] = {};
     const int q_instr = (n + 255) / 256;
     // Issues the block at the cursor into ring slot `slot` and returns where
     // it lies; past the range's end nothing is issued. The first block of a
@@ -1363,17 +1474,26 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
         if (pi >= p_end) return r;
         if (pi == p_first || r.blk == 0) {
             load_q(r, q_in);
-            q_in ^= 1;
             vm_ops += q_instr;
+            q_in ^= 1;
         }
-        const char* src = reinterpret_cast<const char*>(a.k) +
-                          (((size_t)r.slot * kv + r.h) * nblk_cap + r.blk) * (size_t)BB;
         char* dst = &ring[wave][slot][0];
+        // One buffer resource over the (slot, kv head)'s blocks; the block
+        // offset and the 1 KB steps are scalar, so the loads cost no VALU.
+        const int hs_i = __builtin_amdgcn_readfirstlane(r.slot * kv + r.h);
+        const char* hbase = reinterpret_cast<const char*>(a.k) + (size_t)hs_i * (size_t)nblk_cap * BB;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char*>(hbase), 0, (int)(nblk_cap * BB), 0x00020000);
+        const int soff = __builtin_amdgcn_readfirstlane(r.blk) * BB;
+        // The instruction's immediate offset would move the LDS address as
+        // well as the global one: the 1 KB steps go into the scalar offset.
+        const int vo = 16 * lane;
 #pragma unroll
         for (int i = 0; i < CODE_I; ++i)
-            __builtin_amdgcn_global_load_lds(src + 1024 * i + 16 * lane, dst + 1024 * i, 16, 0, AUX_STREAM);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst + 1024 * i, 16, vo, soff + 1024 * i, 0, AUX_STREAM);
+        static_assert(CODE_I == 4 || CODE_I == 8, "code loads per block");
         if (lane < SCL_L)
-            __builtin_amdgcn_global_load_lds(src + 64 * HD + 16 * lane, dst + 64 * HD, 16, 0, AUX_STREAM);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst + 64 * HD, 16, 16 * lane, soff + 64 * HD, 0, AUX_STREAM);
         vm_ops += LPB;
         mark[slot] = vm_ops;
         if (pi + 1 < p_end) step(ci);
@@ -1390,20 +1510,42 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     // position, or -1.
     long pend0 = -1, pend1 = -1;
 
-    SkPos r0 = issue(0);
-    SkPos r1 = issue(1);
+    // A partial of a head, O [g][HD] and (m, l) [g], into this wave's slot sl
+    // with agent-scope (coherent) stores.
+    auto publish = [&](int sl, const floatx4 (&ov)[NT], float m, float l) __attribute__((always_inline)) {
+        const size_t slot_i = (size_t)u * 2 + sl;
+        float* po = a.part + slot_i * (16 * HD);
+        float* pml = a.part + a.ml_off + slot_i * 32;
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(po, 0, 16 * HD * 4, 0x00020000);
+        typedef float v4 __attribute__((ext_vector_type(4)));
+        if (col < group) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                __builtin_amdgcn_raw_buffer_store_b128(v4{ov[t][0], ov[t][1], ov[t][2], ov[t][3]}, rp,
+                                                       (col * HD + 16 * t + 4 * grp) * 4, 0, 16);  // sc1
+            if (grp == 0) {
+                typedef float v2 __attribute__((ext_vector_type(2)));
+                const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(pml, 0, 128, 0x00020000);
+                __builtin_amdgcn_raw_buffer_store_b64(v2{m, l}, rm, 8 * col, 0, 16);  // sc1
+            }
+        }
+    };
+    // The range's first segment when it is part of a head.
+    floatx4 o0[NT];
+    float m_first = 0.0f, l_first = 0.0f;
+
+    SkPos rs[RING];
+#pragma unroll
+    for (int i = 0; i < RING; ++i) rs[i] = issue(i);
 
     // Fold of the block in ring slot `slot` at flat position pp; rn: the
     // position of the block issued into the slot afterwards.
     auto fold_at = [&](int slot, long pp, const SkPos r, SkPos& rn) {
         // This block has landed once at most the instructions issued after
-        // its loads are outstanding.
-        // Rounded down to three levels (a smaller count only waits longer):
-        // nothing after it (the range's last block), the steady state (the
-        // next block's loads), and after a publish (its stores too).
-        const int after = __builtin_amdgcn_readfirstlane(vm_ops - (slot ? mark[1] : mark[0]));
-        if (after >= LPB + NT) wait_vm<LPB + NT>();
-        else if (after >= LPB) wait_vm<LPB>();
+        // its loads are outstanding: nothing, or a whole head's context
+        // stores (rounded down; a smaller count only waits longer).
+        const int after = __builtin_amdgcn_readfirstlane(vm_ops - mark[slot]);
+        if (after >= NT) wait_vm<NT>();
         else wait_vm<0>();
         Frag<HD, KIND> f;
         ring_read<HD>(lds_addr(&ring[wave][slot][0]), lane, grp, f);
@@ -1435,13 +1577,13 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
             l_run = 0.0f;
         }
         // The slot (and the query buffer) are read: refill the slot with the
-        // block two ahead.
+        // next block.
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
         rn = issue(slot);
         if (r.blk == r.nb - 1 && (r.tk & 31))
-            fold_block<HD, KIND, true>(f, qh, ql, r.blk * 32, r.tk, grp, a.score_l2, m_run, l_run, o);
+            fold_block_q8<HD, true>(f, qh, ql, r.blk * 32, r.tk, grp, m_run, l_run, o);
         else
-            fold_block<HD, KIND, false>(f, qh, ql, r.blk * 32, r.tk, grp, a.score_l2, m_run, l_run, o);
+            fold_block_q8<HD, false>(f, qh, ql, r.blk * 32, r.tk, grp, m_run, l_run, o);
         // The end of a segment: a head's last block, or the range's.
         if (r.blk == r.nb - 1 || pp == p_end - 1) {
             const float lsum = sum4grp(l_run);
@@ -1456,39 +1598,35 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
                 }
                 vm_ops += NT;
             } else {
-                // Part of a head: O [g][HD] and (m, l) [g] into this wave's
-                // slot, with agent-scope (coherent) stores.
-                const int sl = pp == p_end - 1 ? 1 : 0;
-                const size_t slot_i = (size_t)u * 2 + sl;
-                float* po = a.part + slot_i * (16 * HD);
-                float* pml = a.part + a.ml_off + slot_i * 32;
-                const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(po, 0, 16 * HD * 4, 0x00020000);
-                typedef float v4 __attribute__((ext_vector_type(4)));
-                if (col < group) {
-#pragma unroll
-                    for (int t = 0; t < NT; ++t)
-                        __builtin_amdgcn_raw_buffer_store_b128(v4{o[t][0], o[t][1], o[t][2], o[t][3]}, rp,
-                                                               (col * HD + 16 * t + 4 * grp) * 4, 0, 16);  // sc1
-                    if (grp == 0) {
-                        typedef float v2 __attribute__((ext_vector_type(2)));
-                        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(pml, 0, 128, 0x00020000);
-                        __builtin_amdgcn_raw_buffer_store_b64(v2{m_run, lsum}, rm, 8 * col, 0, 16);  // sc1
-                    }
-                }
-                vm_ops += NT + 1;
+                // Part of a head. The range's last segment is published at
+                // once (the range ends here); its first one is kept in
+                // registers and published after the range: a store here
+                // would hold every later block's wait (vector-memory
+                // operations retire in issue order) for its write-through.
                 const long hs = rdlane64(sq.base, r.s) + (long)r.h * r.nb;
-                if (sl) pend1 = hs;
-                else pend0 = hs;
+                if (pp == p_end - 1) {
+                    publish(1, o, m_run, lsum);
+                    pend1 = hs;
+                } else {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) o0[t] = o[t];
+                    m_first = m_run;
+                    l_first = lsum;
+                    pend0 = hs;
+                }
             }
         }
     };
 
-    for (long p = p_first; p < p_end; p += 2) {
-        fold_at(0, p, r0, r0);
-        if (p + 1 >= p_end) break;
-        fold_at(1, p + 1, r1, r1);
+    for (long p = p_first; p < p_end; p += RING) {
+#pragma unroll
+        for (int i = 0; i < RING; ++i) {
+            if (p + i >= p_end) break;
+            fold_at(i, p + i, rs[i], rs[i]);
+        }
     }
 
+    if (pend0 >= 0) publish(0, o0, m_first, l_first);
     // Arrivals: after every partial store has completed, count this wave at
     // each head it published part of (at most two), both atomics in one round
     // trip; the last arriver at a head merges it.
@@ -1535,12 +1673,87 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     const bool m1 = pend1 >= 0 && prev1 == (unsigned)(h1.c1 - h1.c0);
     if (!m0 && !m1) return;
     // The heads to merge: A, then B when there are two.
-    const int nm = (int)m0 + (int)m1;
-    const Head A = m0 ? h0 : h1, B = h1;
-    const long cntA = A.c1 - A.c0 + 1, cntB = nm > 1 ? B.c1 - B.c0 + 1 : 0;
+    const int nm_all = (int)m0 + (int)m1;
+    const Head A0 = m0 ? h0 : h1, B0 = h1;
     auto slot_of = [&](const Head& h, long c) -> size_t {
         return (size_t)c * 2 + (c < h.c1 ? 1 : h.last_sl);
     };
+    // A head of at most KF contributors and a context of at most 512 floats
+    // is merged straight from registers: every contributor's O columns and
+    // (m, l) pairs are loaded at once (both heads' together), then, per head
+    // and in range order, M = max m, w = 2^(m - M), l = sum w l, O = sum w O.
+    // Which path a head takes depends on the head alone, and the two heads'
+    // arithmetic never mixes, so a head's bits do not depend on the wave
+    // that merges it or on what it merges beside.
+    constexpr int KF = 10;
+    const bool fit = n <= 512;
+    const bool fa = fit && A0.c1 - A0.c0 + 1 <= KF, fb = fit && nm_all > 1 && B0.c1 - B0.c0 + 1 <= KF;
+    if (fa || fb) {
+        const Region pr = region(a.part, (uint32_t)((a.ml_off + (long)a.items * W * 2 * 32) * 4));
+        const Head F0 = fa ? A0 : B0, F1 = B0;
+        const int nf = (int)fa + (int)fb;
+        const int c0n = (int)(F0.c1 - F0.c0 + 1), c1n = nf > 1 ? (int)(F1.c1 - F1.c0 + 1) : 0;
+        int e4[2], g[2];
+        bool on[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            e4[j] = lane + 64 * j;
+            on[j] = e4[j] < n / 4;
+            g[j] = on[j] ? (4 * e4[j]) / HD : 0;
+        }
+        floatx4 ov[2][KF][2];
+        float2 mv[2][KF][2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const Head& H = hh ? F1 : F0;
+            const int cn = hh ? c1n : c0n;
+#pragma unroll
+            for (int k = 0; k < KF; ++k) {
+                if (k < cn) {
+                    const uint32_t si = (uint32_t)__builtin_amdgcn_readfirstlane((int)slot_of(H, H.c0 + k));
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const float4 x = ld_region4<AUX_AGENT>(pr, (si * (16 * HD) + 4 * (on[j] ? e4[j] : 0)) * 4);
+                        ov[hh][k][j] = floatx4{x.x, x.y, x.z, x.w};
+                        mv[hh][k][j] = ld_region2<AUX_AGENT>(pr, (uint32_t)(a.ml_off + si * 32 + 2 * g[j]) * 4);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            if (hh >= nf) continue;
+            const Head& H = hh ? F1 : F0;
+            const int cn = hh ? c1n : c0n;
+            float* out = a.out + a.out_off + (size_t)(H.idx / kv) * a.out_stride + (size_t)(H.idx % kv) * n;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float M = ninf();
+#pragma unroll
+                for (int k = 0; k < KF; ++k)
+                    if (k < cn) M = fmaxf(M, mv[hh][k][j].x);
+                float L = 0.0f;
+                floatx4 acc = zero_f4();
+#pragma unroll
+                for (int k = 0; k < KF; ++k) {
+                    if (k < cn) {
+                        const float w = ex2(mv[hh][k][j].x - M);
+                        L = __builtin_fmaf(mv[hh][k][j].y, w, L);
+                        acc[0] = __builtin_fmaf(ov[hh][k][j][0], w, acc[0]);
+                        acc[1] = __builtin_fmaf(ov[hh][k][j][1], w, acc[1]);
+                        acc[2] = __builtin_fmaf(ov[hh][k][j][2], w, acc[2]);
+                        acc[3] = __builtin_fmaf(ov[hh][k][j][3], w, acc[3]);
+                    }
+                }
+                if (on[j]) *reinterpret_cast<floatx4*>(out + 4 * e4[j]) = acc * (1.0f / L);
+            }
+        }
+    }
+    // The heads left to the general merge.
+    const bool ga = !fa, gb = nm_all > 1 && !fb;
+    const int nm = (int)ga + (int)gb;
+    const Head A = ga ? A0 : B0, B = B0;
+    const long cntA = nm ? A.c1 - A.c0 + 1 : 0, cntB = nm > 1 ? B.c1 - B.c0 + 1 : 0;
     // Each head's contributors are merged, in range order, in chunks of KC
     // counted from the head's first: a chunk's (m, l) pairs go straight into
     // LDS (half of the wave's idle ring per head, lane-strided dword loads),
@@ -1551,13 +1764,13 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     // one list), two float4 loads each: with the (m, l) loads at most ~60
     // vector-memory instructions, under the 63 a wave can have outstanding.
     // Lane owns float4 e4 = lane + 64 j of a head's [g][HD] context.
-    constexpr int HALF_F = ((2 * BB / 4 - 64) / 2) / 64 * 64;  // floats of LDS per head
+    constexpr int HALF_F = ((RING * BB / 4 - 64) / 2) / 64 * 64;  // floats of LDS per head
     const int gp = 2 * group;                            // (m, l) floats per contributor
     const int KC = HALF_F / gp;
     float* const mls = reinterpret_cast<float*>(&ring[wave][0][0]);
     float* const Ms = mls + 2 * HALF_F;  // [head][16]: the chunk's running max per query head
     const float* const mlp = a.part + a.ml_off;
-    for (int j0 = 0; j0 * 64 < n / 4; j0 += 2) {
+    for (int j0 = 0; nm > 0 && j0 * 64 < n / 4; j0 += 2) {
         int e4[2], g[2];
         bool on[2];
 #pragma unroll
@@ -1672,6 +1885,8 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
             };
             // Most merges hold at most 8 contributors: a batch of 8 keeps
             // their loads, LDS reads and folds to what they use.
+            for (int cb = 0; cb < nc; cb += 8) batch(std::integral_constant<int, 8>{}, cb);
+            if (0)
             if (nc <= 8) batch(std::integral_constant<int, 8>{}, 0);
             else
                 for (int cb = 0; cb < nc; cb += 24) batch(std::integral_constant<int, 24>{}, cb);
@@ -1687,9 +1902,9 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
         }
     }
     if (lane == 0) {
-        __hip_atomic_store(a.ctr + (size_t)A.idx * CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (nm > 1)
-            __hip_atomic_store(a.ctr + (size_t)B.idx * CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.ctr + (size_t)A0.idx * CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (nm_all > 1)
+            __hip_atomic_store(a.ctr + (size_t)B0.idx * CTR_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1715,13 +1930,14 @@ static hipError_t launch_merge(int hd, const DecodeArgs& a, int kv_heads, int ns
 static hipError_t launch_attn(int hd, int kind, const DecodeArgs& a, int kv_heads, int nseq, hipStream_t st) {
     if (a.sk) {
         dim3 grid(a.items), block(DT);
-        if (kind != KV_TQ8) return hipErrorInvalidValue;
-        const size_t qdyn = (size_t)DW * 2 * a.group * hd * sizeof(float);  // raw query buffers (<= 64 KB)
+        if (kind != KV_TQ8 || !(hd == 64 || hd == 128)) return hipErrorInvalidValue;
+        // The raw query buffers; with the static ring, never over a
+        // workgroup's LDS (the entry point refuses larger groups first).
+        const size_t qdyn = sk_qdyn_bytes(hd, a.group);
+        if (sk_lds_bytes(hd, a.group) > SK_LDS_MAX) return hipErrorInvalidValue;
         if (hd == 128) hipLaunchKernelGGL((attn_decode_sk_kernel<128>), grid, block, qdyn, st, a);
-        else if (hd == 64) hipLaunchKernelGGL((attn_decode_sk_kernel<64>), grid, block, qdyn, st, a);
-        else return hipErrorInvalidValue;
+        else hipLaunchKernelGGL((attn_decode_sk_kernel<64>), grid, block, qdyn, st, a);
         return hipGetLastError();
-        return hipErrorInvalidValue;
     }
     const dim3 grid = a.xcd ? dim3(a.splits * kv_heads * nseq) : dim3(a.splits, kv_heads, nseq);
     dim3 block(DT);
