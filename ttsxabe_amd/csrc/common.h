@@ -19,6 +19,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 typedef _Float16 half_t;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -174,4 +177,16 @@ __device__ __forceinline__ float2 ld_region2(const Region& g, uint32_t off) {
     typedef float v2 __attribute__((ext_vector_type(2)));
     const v2 x = __builtin_amdgcn_raw_buffer_load_b64(g.r, off, 0, AUX);
     return make_float2(x[0], x[1]);
+}
+
+// Calls f(std::integral_constant<int, i>{}) for i = 0 .. N-1, unrolled, so a
+// loop index can select registers (an index chosen at run time would put a
+// register array in scratch).
+template <int... I, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, F&& f) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(std::make_integer_sequence<int, N>{}, f);
 }

@@ -39,6 +39,11 @@
 // tile loop's software pipeline, at most the pipeline's reads (measured on
 // MI355X: 4 -> 6 -> 10 took C3@512 14.5 -> 14.0 -> 13.8 us and C3@8192
 // 631 -> 613 -> 611 us; 12 and 16 were slower again).
+// Staged (f32) encoder rows: tiles whose loads are in flight ahead of the
+// one being written to LDS.
+#ifndef LLMTIE_PF_SPD
+#define LLMTIE_PF_SPD 2
+#endif
 #ifndef LLMTIE_PF_PD
 #define LLMTIE_PF_PD 10
 #endif
@@ -470,7 +475,14 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
     const size_t svb = KIND == PF_ROWS ? (size_t)kh * HD : (size_t)kh * HD * a.cap;  // V: head base
     const bool vvec = KIND == PF_F32 && a.cap % 4 == 0;  // V^T rows 16-byte aligned
     constexpr int NSR = STAGED ? NF : 1;
-    float4 sr[NSR][2];
+    // Staged tiles in flight: tile j's f32 loads are issued SPD periods
+    // before it is written to LDS (the K/V rows come from L2 or the Infinity
+    // Cache, whose latency is several tiles' compute at the encoder's
+    // shape). SPD register sets rotate, so the period loop is unrolled by
+    // SU = lcm(SPD, 2) (the two LDS buffers).
+    constexpr int SPD = KIND == PF_ROWS ? LLMTIE_PF_SPD : 1;
+    constexpr int SU = SPD % 2 == 0 ? SPD : 2 * SPD;
+    float4 sr[SPD][NSR][2];
     // Stacked rows: V is [key][dim], so a thread takes 4 dims x VR keys
     // (one float4 from each of VR rows; 16 threads cover one 256-byte row
     // segment) instead of one fragment chunk, and writes each dim's VR keys
@@ -480,14 +492,15 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
     constexpr int VR = 1024 / TW;      // rows V: keys per thread (4, or 2 at eight waves)
     static_assert(KIND != PF_ROWS || (HD == 64 && KF % W == 0 && 2 * (NF - KI) == VR), "rows: hd 64");
     const int rdq = tid & 15, kb = VR * (tid >> 4);  // rows V: dims 4*rdq .. +3, keys kb .. kb + VR - 1
-    auto stage_load = [&](int kv0) __attribute__((always_inline)) {
+    auto stage_load = [&](auto set_tag, int kv0) __attribute__((always_inline)) {
+        constexpr int SS = decltype(set_tag)::value;
         if constexpr (KIND == PF_ROWS) {
 #pragma unroll
             for (int u = 0; u < VR; ++u) {
                 const int key = kv0 + kb + u;
                 const float4 x = *reinterpret_cast<const float4*>(vf32 + svb + (size_t)min(key, ktot - 1) * a.kvs +
                                                                   4 * rdq);
-                sr[KI + u / 2][u % 2] = key < ktot ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+                sr[SS][KI + u / 2][u % 2] = x;  // zeroed past the keys when stored
             }
         }
         if constexpr (STAGED) {
@@ -495,13 +508,16 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
             for (int i = 0; i < NF; ++i) {
                 const int f = wave + W * i;
                 if (KIND == PF_ROWS && i >= KI) continue;
-                if (f < KF) {
+                // Rows: the K fragments are the first KI = KF / W slots of
+                // every wave, never a V one (so no dead V branch sits between
+                // the loads and leaves their waits conservative).
+                if (KIND == PF_ROWS || f < KF) {
                     const int hf = f / (2 * NS), T = (f / NS) & 1, s = f % NS;
                     const int key = min(kv0 + 32 * hf + 8 * (col >> 2) + 4 * T + (col & 3), ktot - 1);
                     const float4* p = reinterpret_cast<const float4*>(kf32 + skb + (size_t)key * skr + 32 * s + 8 * grp);
-                    sr[i][0] = p[0];
-                    sr[i][1] = p[1];
-                } else {
+                    sr[SS][i][0] = p[0];
+                    sr[SS][i][1] = p[1];
+                } else if constexpr (KIND != PF_ROWS) {
                     const int fv = f - KF, hf = fv / NT, t = fv % NT;
                     const int d = 16 * t + col, k0 = kv0 + 32 * hf + 8 * grp;
                     float4 v0, v1;
@@ -519,20 +535,22 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
                         v0 = make_float4(x[0], x[1], x[2], x[3]);
                         v1 = make_float4(x[4], x[5], x[6], x[7]);
                     }
-                    sr[i][0] = v0;
-                    sr[i][1] = v1;
+                    sr[SS][i][0] = v0;
+                    sr[SS][i][1] = v1;
                 }
             }
         }
     };
-    auto stage_store = [&](half_t* dst) __attribute__((always_inline)) {
+    auto stage_store = [&](auto set_tag, half_t* dst, int kv0) __attribute__((always_inline)) {
+        constexpr int SS = decltype(set_tag)::value;
         if constexpr (KIND == PF_ROWS) {
             // Dim 4*rdq + e, keys kb .. kb + VR - 1: V fragment (half, t) =
             // (kb / 32, dim / 16), lane (dim % 16) + 16 * ((kb / 8) % 4), halves kb % 8 ..
             typedef _Float16 hv __attribute__((ext_vector_type(VR)));
             float4 x[VR];
 #pragma unroll
-            for (int u = 0; u < VR; ++u) x[u] = sr[KI + u / 2][u % 2];
+            for (int u = 0; u < VR; ++u)
+                x[u] = kv0 + kb + u < ktot ? sr[SS][KI + u / 2][u % 2] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int dd = 4 * rdq + e;
@@ -553,7 +571,7 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
             for (int i = 0; i < NF; ++i) {
                 const int f = wave + W * i;
                 if (KIND == PF_ROWS && i >= KI) continue;
-                const float4 x0 = sr[i][0], x1 = sr[i][1];
+                const float4 x0 = sr[SS][i][0], x1 = sr[SS][i][1];
                 half8 y;
                 y[0] = to_h(x0.x); y[1] = to_h(x0.y); y[2] = to_h(x0.z); y[3] = to_h(x0.w);
                 y[4] = to_h(x1.x); y[5] = to_h(x1.y); y[6] = to_h(x1.z); y[7] = to_h(x1.w);
@@ -595,7 +613,9 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
     // use waits for every load issued before it, tile loads included: the
     // compiler does not count LDS-DMA loads in order).
     if constexpr (STAGED) {
-        if (kend > 0) stage_load(0);
+        // Unconditional (rows past the keys are clamped to the last one), so
+        // no branch leaves the compiler unsure how many loads are pending.
+        if (kend > 0) static_for<SPD>([&](auto i) { stage_load(i, decltype(i)::value * KT); });
     } else {
         if (kend > 0) issue(0, t0);
     }
@@ -781,29 +801,33 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
     };
 
     // Staged kinds: tile j is in LDS buffer `cur` when the barrier passes;
-    // tile j + 1's f32 loads are in flight in registers while tile j is
-    // computed, then rounded and written to `nxt`, which every wave finished
-    // reading before that barrier.
-    auto step_staged = [&](half_t* cur, half_t* nxt, int kv0) __attribute__((always_inline)) {
+    // tile j + SPD's f32 loads go out into the register set tile j left
+    // (written to LDS at the end of the period before), tile j is computed,
+    // then tile j + 1 (loaded SPD - 1 periods ago) is rounded and written to
+    // `nxt`, which every wave finished reading before that barrier.
+    auto step_staged = [&](auto jj_tag, half_t* cur, half_t* nxt, int kv0) __attribute__((always_inline)) {
+        constexpr int JJ = decltype(jj_tag)::value;
         __syncthreads();
-        const bool more = kv0 + KT < kend;
-        if (more) stage_load(kv0 + KT);
+        stage_load(std::integral_constant<int, JJ % SPD>{}, kv0 + SPD * KT);
         __builtin_amdgcn_sched_barrier(0);
-        if (kv0 <= wlim) {
+        if (kv0 <= wlim && kv0 < kend) {
             if (kv0 + KT - 1 > wall)
                 tile(cur, kv0, std::true_type{});
             else
                 tile(cur, kv0, std::false_type{});
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (more) stage_store(nxt);
+        stage_store(std::integral_constant<int, (JJ + 1) % SPD>{}, nxt, kv0 + KT);
     };
     if constexpr (STAGED) {
-        if (kend > 0) stage_store(t0);
-        for (int kv0 = 0; kv0 < kend; kv0 += 2 * KT) {
-            step_staged(t0, t1, kv0);
-            if (kv0 + KT < kend) step_staged(t1, t0, kv0 + KT);
-        }
+        if (kend > 0) stage_store(std::integral_constant<int, 0>{}, t0, 0);
+        // Whole rounds of SU periods; the periods past the last tile only
+        // load clamped rows and write a tile nobody reads.
+        for (int kv0 = 0; kv0 < kend; kv0 += SU * KT)
+            static_for<SU>([&](auto jj) {
+                constexpr int JJ = decltype(jj)::value;
+                step_staged(jj, JJ % 2 ? t1 : t0, JJ % 2 ? t0 : t1, kv0 + JJ * KT);
+            });
     } else {
         for (int kv0 = 0; kv0 < kend; kv0 += 2 * KT) {
             step(t0, t1, kv0);
