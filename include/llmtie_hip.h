@@ -55,8 +55,11 @@ typedef enum llmtie_status {
     LLMTIE_SCRATCH_GROWTH_IN_CAPTURE = 11, /* a decode scratch would have to grow while its stream captures a
                                             * graph (no reference twin: the reference does not capture);
                                             * fields: partial floats needed, held, counters needed, held */
-    LLMTIE_SCRATCH_LIMIT = 12              /* the fixed scratch of llmtie_attn_decode_f16_noalloc is too small
+    LLMTIE_SCRATCH_LIMIT = 12,             /* the fixed scratch of llmtie_attn_decode_f16_noalloc is too small
                                             * for the call (no reference twin); fields as above */
+    LLMTIE_SPLIT_HEAD_LOST = 13            /* an earlier decode through this scratch wrote NaN for a head whose
+                                            * split workgroups did not share an XCD (no reference twin; see
+                                            * llmtie_decode_scratch_status); no fields */
 } llmtie_status;
 
 /* The last error raised on the calling thread: the status, up to four numeric
@@ -77,15 +80,34 @@ const char* llmtie_version(void);
  * and owned by the caller. Replaces `DecodeScratch::new()` (device.rs:219).
  * Its counters start at zero and every call leaves them at zero.
  * Graphs: a call captured into a HIP graph records the scratch's buffers.
- * Growth never frees a buffer: the replaced one stays allocated until
- * llmtie_decode_scratch_free (the 64 most recent; an older one is released
- * after a device synchronisation), so an earlier graph keeps replaying
- * correctly. Growth is refused while the stream is capturing
+ * Growth never frees a buffer: every replaced one stays allocated until
+ * llmtie_decode_scratch_free, so an earlier graph keeps replaying correctly.
+ * Growth is refused while the stream is capturing
  * (LLMTIE_SCRATCH_GROWTH_IN_CAPTURE): make one eager call of the largest shape
  * first. Freeing the scratch invalidates every graph that used it. */
 typedef struct llmtie_decode_scratch llmtie_decode_scratch;
 llmtie_decode_scratch* llmtie_decode_scratch_new(void);
 void llmtie_decode_scratch_free(llmtie_decode_scratch* s);
+
+/* The XCD-local split hand-off (no reference twin). When every XCD's run of a
+ * launch's workgroups holds whole heads, a head's split partials pass
+ * through that XCD's L2 instead of memory. The kernel checks that each head's
+ * workgroups really shared an XCD; a head whose did not is written as NaN
+ * (its int8 twin with NaN scales), never as a silently wrong context, and the
+ * scratch records it in a host-visible word. The next decode call through the
+ * scratch then returns LLMTIE_SPLIT_HEAD_LOST without launching, and
+ * llmtie_decode_scratch_status returns (and clears) the same status after a
+ * stream synchronisation; LLMTIE_OK otherwise. No failure has been seen on
+ * gfx950, whose dispatcher deals workgroups L and L + 8k to one XCD; the
+ * environment variable LLMTIE_DECODE_XCD=0 selects the coherent hand-off
+ * everywhere (about 2 % slower at C2). The no-allocation entry point always
+ * uses the coherent hand-off. */
+int llmtie_decode_scratch_status(llmtie_decode_scratch* s);
+
+/* Test hook (no reference twin; never needed in use): nonzero makes every
+ * later decode report fake XCC ids (workgroup L as (L / 8) % 8) to the
+ * XCD-local check, so a test can drive the check's failure path. */
+void llmtie_debug_fake_xcc(int on);
 
 /* ---------------------------------------------------------------- prefill */
 

@@ -161,3 +161,31 @@ def test_the_batched_q8_decode_refuses_groups_over_its_lds_budget():
     cap = (2**31 // 8704 + 1) * 32
     assert L.llmtie_attn_decode_q8_batch(NULL, P, BIG, P, BIG, 1, P, P, 1, 64, 32, 8, 128, cap,
                                          C.c_float(0.1), 0, P, P, BIG) == 3
+
+
+def test_the_decode_boundary_accepts_its_documented_superset():
+    """Wider than the reference's refusals, by design (the header says so):
+    the f32-cache decode takes head_dim 128 as well as 64, and every decode
+    takes GQA groups up to 16 (the reference: up to 4, 8 for its h64 g8
+    kernel). Such shapes pass every shape check and reach the scratch check
+    (a null scratch is refused as an invalid argument, status 10), where the
+    reference would refuse them as UnsupportedAttention (status 1)."""
+    L = _lib.lib()
+    BIG = 10**12
+    P = 4096
+    # attn_decode (f32 cache) at head_dim 128, group 4.
+    assert L.llmtie_attn_decode(NULL, P, BIG, P, BIG, P, BIG, 32, 8, 128, 100, 128, C.c_float(0.1), 0,
+                                NULL, P, BIG) == 10
+    # attn_decode_f16 at a group of 16.
+    assert L.llmtie_attn_decode_f16(NULL, P, BIG, P, BIG, P, BIG, 32, 2, 128, 100, 128, C.c_float(0.1), 0,
+                                    NULL, P, BIG) == 10
+    # ... and still refused past 16, and at a head width with no kernel.
+    assert L.llmtie_attn_decode_f16(NULL, P, BIG, P, BIG, P, BIG, 34, 2, 128, 100, 128, C.c_float(0.1), 0,
+                                    NULL, P, BIG) == 1
+    assert L.llmtie_attn_decode(NULL, P, BIG, P, BIG, P, BIG, 8, 8, 96, 100, 128, C.c_float(0.1), 0,
+                                NULL, P, BIG) == 1
+
+
+def test_a_scratch_with_no_lost_head_reports_ok():
+    L = _lib.lib()
+    assert L.llmtie_decode_scratch_status(NULL) == 0

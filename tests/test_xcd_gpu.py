@@ -19,13 +19,13 @@ from tests.util import down, up, up_f16
 pytestmark = pytest.mark.gpu
 
 
-def _c2(gpu, tiled):
+def _c2(gpu, tiled, s=None):
     from ttsxabe_amd.gpu import DecodeScratch, TiledCache16
     heads, kv, hd, tk, cap = 32, 8, 128, 4096, 4096
     q = up(oracle.seq(heads * hd, 41))
     k = up_f16(oracle.seq(kv * cap * hd, 42))
     v = up_f16(oracle.seq(kv * cap * hd, 43))
-    s = DecodeScratch()
+    s = s or DecodeScratch()
     if tiled:
         t = TiledCache16(kv, hd, cap)
         gpu.t16_from_ref(k, v, t, tk)
@@ -43,12 +43,33 @@ def test_the_xcd_local_hand_off_matches_the_coherent_one(gpu, tiled, monkeypatch
     assert np.array_equal(local.view(np.uint32), coherent.view(np.uint32))
 
 
-def test_a_head_spread_over_xcds_is_nan_not_wrong(gpu, monkeypatch):
-    run = _c2(gpu, True)
+def test_a_head_spread_over_xcds_is_nan_and_reported(gpu):
+    """Faked XCC ids (the test hook) make every merged head fail the check:
+    its context is NaN, the scratch's status says so (and is cleared by
+    reading it), the next call through the scratch is refused with the same
+    status before it launches, and the counters are left clean."""
+    from ttsxabe_amd import _lib
+    from ttsxabe_amd.gpu import DecodeScratch, SplitHeadLost
+    s = DecodeScratch()
+    run = _c2(gpu, True, s)
     good = run()
-    monkeypatch.setenv("LLMTIE_DECODE_XCD_FAKE", "1")  # workgroup L reports XCC id (L / 8) % 8
-    bad = run()
+    s.check()
+    _lib.lib().llmtie_debug_fake_xcc(1)  # workgroup L reports XCC id (L / 8) % 8
+    try:
+        bad = run()
+    finally:
+        _lib.lib().llmtie_debug_fake_xcc(0)
     assert np.isnan(bad).all(), "every head of C2 is merged across splits"
-    monkeypatch.delenv("LLMTIE_DECODE_XCD_FAKE")
-    again = run()  # the counters were reset by the NaN path
+    with pytest.raises(SplitHeadLost):
+        run()  # refused: the earlier call lost heads
+    again = run()  # the refusal cleared the status; the counters were reset by the NaN path
     assert np.array_equal(good.view(np.uint32), again.view(np.uint32))
+    _lib.lib().llmtie_debug_fake_xcc(1)
+    try:
+        run()
+    finally:
+        _lib.lib().llmtie_debug_fake_xcc(0)
+    torch.cuda.synchronize()
+    with pytest.raises(SplitHeadLost):
+        s.check()
+    s.check()  # cleared

@@ -30,6 +30,8 @@ SIGNATURES = {
     "llmtie_version": (C.c_char_p, []),
     "llmtie_decode_scratch_new": (P, []),
     "llmtie_decode_scratch_free": (None, [P]),
+    "llmtie_decode_scratch_status": (I, [P]),
+    "llmtie_debug_fake_xcc": (None, [I]),
     "llmtie_supports_flash": (I, [SZ, SZ, SZ]),
     "llmtie_flash_attn": (I, [P, P, SZ, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, SZ, F, I]),
     "llmtie_flash_attn_f16": (I, [P, P, SZ, P, SZ, P, SZ, P, SZ, SZ, SZ, SZ, SZ, SZ, SZ, F, I]),

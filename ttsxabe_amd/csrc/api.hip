@@ -9,7 +9,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <mutex>
+#include <vector>
 
 #include "../../include/llmtie_hip.h"
 #include "decode.h"
@@ -22,6 +24,8 @@ using namespace llmtie;
 namespace {
 
 thread_local llmtie_error g_err = {0, {0, 0, 0, 0}, {0}};
+// llmtie_debug_fake_xcc: the test hook for the XCD-local check.
+std::atomic<bool> g_fake_xcc{false};
 
 int fail(int status, size_t f0, size_t f1, size_t f2, size_t f3, const char* fmt, ...) {
     g_err.status = status;
@@ -99,8 +103,10 @@ struct llmtie_decode_scratch {
     int device = -1;
     // Buffers replaced by growth. A HIP graph captured with the scratch keeps
     // their addresses, so they stay allocated until the scratch is freed.
-    void* retired[64] = {nullptr};
-    int nretired = 0;
+    std::vector<void*> retired;
+    // Host-visible word (pinned host memory) the decode kernel sets when an
+    // XCD-local head's split workgroups turn out not to share an XCD.
+    unsigned* lost = nullptr;
 };
 
 extern "C" {
@@ -118,9 +124,20 @@ void llmtie_decode_scratch_free(llmtie_decode_scratch* s) {
     if (!s) return;
     if (s->part) (void)hipFree(s->part);
     if (s->ctr) (void)hipFree(s->ctr);
-    for (int i = 0; i < s->nretired; ++i) (void)hipFree(s->retired[i]);
+    for (void* p : s->retired) (void)hipFree(p);
+    if (s->lost) (void)hipHostFree(s->lost);
     delete s;
 }
+
+int llmtie_decode_scratch_status(llmtie_decode_scratch* s) {
+    if (!s || !s->lost || !__atomic_load_n(s->lost, __ATOMIC_ACQUIRE)) return LLMTIE_OK;
+    __atomic_store_n(s->lost, 0u, __ATOMIC_RELEASE);
+    return fail(LLMTIE_SPLIT_HEAD_LOST, 0, 0, 0, 0,
+                "an earlier decode through this scratch wrote NaN for a head whose split workgroups did not "
+                "share an XCD; LLMTIE_DECODE_XCD=0 selects the coherent hand-off");
+}
+
+void llmtie_debug_fake_xcc(int on) { g_fake_xcc.store(on != 0); }
 
 int llmtie_supports_flash(size_t head_dim, size_t heads, size_t kv_heads) {
     return (head_dim == 64 || head_dim == 128) && kv_heads > 0 && heads % kv_heads == 0 && heads > 0;
@@ -265,19 +282,11 @@ int xcd_local(int splits, size_t units, int two_phase) {
     return (total / 8) % (size_t)splits == 0 ? 1 : 0;
 }
 
-// A buffer the scratch no longer uses. It is kept allocated (a graph
-// captured earlier may still read it) until the scratch is freed; past 64
-// retirements the oldest is released after the device has drained.
+// A buffer the scratch no longer uses. It is kept allocated until the
+// scratch is freed: a graph captured earlier may still read it. (Growth is by
+// powers of two, so a scratch retires a few dozen buffers at most.)
 int retire(llmtie_decode_scratch* s, void* p) {
-    if (!p) return LLMTIE_OK;
-    if (s->nretired == 64) {
-        hipError_t e = hipDeviceSynchronize();
-        if (e != hipSuccess) return driver("hipDeviceSynchronize", e);
-        (void)hipFree(s->retired[0]);
-        memmove(s->retired, s->retired + 1, 63 * sizeof(void*));
-        s->nretired = 63;
-    }
-    s->retired[s->nretired++] = p;
+    if (p) s->retired.push_back(p);
     return LLMTIE_OK;
 }
 
@@ -306,6 +315,13 @@ int ensure_scratch(llmtie_decode_scratch* s, size_t part_floats, size_t ctrs, hi
         s->ctr = nullptr;
         s->part_cap = s->ctr_cap = 0;
         s->device = dev;
+    }
+    if (!s->lost) {
+        void* w = nullptr;
+        e = hipHostMalloc(&w, sizeof(unsigned), hipHostMallocMapped | hipHostMallocCoherent);
+        if (e != hipSuccess) return driver("allocating the scratch's status word", e);
+        s->lost = static_cast<unsigned*>(w);
+        *s->lost = 0;
     }
     if (s->part_cap < part_floats) {
         size_t want = 1024;
@@ -392,6 +408,11 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     }
     if (!q || !k || !v || !out) return invalid("a buffer");
     if (!scratch && !noalloc) return invalid("scratch");
+    // A head lost by an earlier call through this scratch (see
+    // llmtie_decode_scratch_status) is reported before anything is launched.
+    if (!noalloc) {
+        if (int r = llmtie_decode_scratch_status(scratch)) return r;
+    }
     const size_t group = heads / kv_heads;
     int nit, splits;
     plan_decode(tk, kv_heads, group, nit, splits);
@@ -443,8 +464,11 @@ int decode_common(void* stream, int kind, const float* q, size_t q_len, size_t q
     a.splits = splits;
     a.ml_stride = (long)mls;
     a.two_phase = two_phase_merge(splits, kv_heads);
-    a.xcd = xcd_local(splits, kv_heads, a.two_phase);
-    a.xcd_fake = getenv("LLMTIE_DECODE_XCD_FAKE") ? 1 : 0;
+    // The no-allocation path has no status word to report a lost head to,
+    // so it always hands partials over coherently.
+    a.xcd = noalloc ? 0 : xcd_local(splits, kv_heads, a.two_phase);
+    a.xcd_fake = g_fake_xcc.load() ? 1 : 0;
+    a.lost = noalloc ? nullptr : scratch->lost;
     return launched("attn_decode", launch_decode((int)hd, kind, a, (int)kv_heads, 1, S(stream)));
 }
 
@@ -531,9 +555,10 @@ namespace {
 std::mutex noalloc_mu;
 float* noalloc_ptr[64];
 
-// This device's copy of `scratch`, its counters cleared on first use (by a
-// kernel on `st`; every call leaves them at zero afterwards).
+// This device's copy of `scratch` (zero at load; every call leaves its
+// counters at zero).
 int noalloc_scratch(hipStream_t st, FixedScratch& f) {
+    (void)st;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return driver("hipGetDevice", e);
@@ -543,8 +568,10 @@ int noalloc_scratch(hipStream_t st, FixedScratch& f) {
         float* p = nullptr;
         e = hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch));
         if (e != hipSuccess) return driver("hipGetSymbolAddress(scratch)", e);
-        e = launch_fill_u32(reinterpret_cast<unsigned*>(p + NOALLOC_PART_FLOATS), NOALLOC_CTR_WORDS, 0u, st);
-        if (e != hipSuccess) return driver("clearing the fixed scratch", e);
+        // No clearing launch: the array has no initialiser, so it is zero
+        // when the code object is loaded (a zero-filled segment), and every
+        // call leaves its counters at zero. A fill here would be recorded
+        // into a graph if this first call were made under stream capture.
         noalloc_ptr[dev] = p;
     }
     f.part = noalloc_ptr[dev];
@@ -617,6 +644,7 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     if (nseq == 0) return ok();
     if (!q || !cache || !tk_dev || !slot_dev || !out) return invalid("a buffer");
     if (!scratch) return invalid("scratch");
+    if (int r = llmtie_decode_scratch_status(scratch)) return r;
     const size_t group = heads / kv_heads;
     int nit, splits;
     plan_decode(max_tk, kv_heads * nseq, group, nit, splits);
@@ -659,7 +687,8 @@ int llmtie_attn_decode_q8_batch(void* stream, const float* q, size_t q_len, cons
     a.ml_stride = (long)mls;
     a.two_phase = sk ? 0 : two_phase_merge(splits, kv_heads * nseq);
     a.xcd = sk ? 0 : xcd_local(splits, kv_heads * nseq, a.two_phase);
-    a.xcd_fake = getenv("LLMTIE_DECODE_XCD_FAKE") ? 1 : 0;
+    a.xcd_fake = g_fake_xcc.load() ? 1 : 0;
+    a.lost = scratch->lost;
     a.sk = sk ? 1 : 0;
     a.nseq = (int)nseq;
     a.items = items;

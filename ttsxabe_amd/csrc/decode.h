@@ -59,6 +59,8 @@ struct DecodeArgs {
     // if not, the head's context is written as NaN, never silently wrong.
     int xcd;
     int xcd_fake;  // tests only: report XCC id (L / 8) % 8 instead of the real one
+    // Pinned host word set (system scope) when a head's check fails, or null.
+    unsigned* lost;
     // Workgroups of the launch / 8, set by launch_decode: the kernel reads it
     // with its other arguments rather than from the dispatch packet (a second
     // scalar-memory round trip before the first K/V load).

@@ -1146,7 +1146,10 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
                 if ((e & 31) == 0) ts[idx >> 5] = __builtin_nanf("");
             }
         }
-        if (tid == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) {
+            __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.lost) __hip_atomic_store(a.lost, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
         return;
     }
     if (loc) merge_head<HD, AUX_XCD>(po, pml, nsplit, group, lds, gl, out, tc, ts, (size_t)h * group * HD);
@@ -1754,15 +1757,16 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
     const int nm = (int)ga + (int)gb;
     const Head A = ga ? A0 : B0, B = B0;
     const long cntA = nm ? A.c1 - A.c0 + 1 : 0, cntB = nm > 1 ? B.c1 - B.c0 + 1 : 0;
-    // Each head's contributors are merged, in range order, in chunks of KC
+    // The general merge (heads of more than KF contributors, or contexts of
+    // more than 512 floats). Each head's contributors are merged, in range order, in chunks of KC
     // counted from the head's first: a chunk's (m, l) pairs go straight into
     // LDS (half of the wave's idle ring per head, lane-strided dword loads),
     // its max M is taken once, and every contributor then adds 2^(m - M)
     // times its l and O. The arithmetic of a head depends only on its own
     // contributors, never on which wave merges it or what it merges beside.
-    // O moves in batches of MB = 8 or 24 contributors (both heads' chunks as
-    // one list), two float4 loads each: with the (m, l) loads at most ~60
-    // vector-memory instructions, under the 63 a wave can have outstanding.
+    // O moves in batches of 8 contributors (both heads' chunks as one list),
+    // two float4 loads each, under the 63 vector-memory instructions a wave
+    // can have outstanding.
     // Lane owns float4 e4 = lane + 64 j of a head's [g][HD] context.
     constexpr int HALF_F = ((RING * BB / 4 - 64) / 2) / 64 * 64;  // floats of LDS per head
     const int gp = 2 * group;                            // (m, l) floats per contributor
@@ -1883,13 +1887,10 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
                 for (int k = 0; k < MB; ++k)
                     if (k >= kA && k < kn) add(acc[1], L[1], k);
             };
-            // Most merges hold at most 8 contributors: a batch of 8 keeps
-            // their loads, LDS reads and folds to what they use.
+            // Batches of 8 contributors: their O registers (64 VGPRs) stay
+            // under the stream loop's own need, so the kernel keeps one
+            // register budget (a batch of 24 set it, with spills).
             for (int cb = 0; cb < nc; cb += 8) batch(std::integral_constant<int, 8>{}, cb);
-            if (0)
-            if (nc <= 8) batch(std::integral_constant<int, 8>{}, 0);
-            else
-                for (int cb = 0; cb < nc; cb += 24) batch(std::integral_constant<int, 24>{}, cb);
         }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {

@@ -23,6 +23,7 @@ from . import _lib
 __all__ = [
     "CudaError", "UnsupportedAttention", "OddCacheCapacity", "CacheOverrun", "SliceOverrun", "RaggedBlock",
     "MismatchedQ8", "OddHeadDim", "Driver", "NoDevice", "InvalidArgument", "ScratchGrowthInCapture", "ScratchLimit",
+    "SplitHeadLost",
     "DecodeScratch",
     "Q8", "KvCacheQ8",
     "TiledCache16", "Gpu",
@@ -89,9 +90,15 @@ class ScratchLimit(CudaError):
     status = 12
 
 
+class SplitHeadLost(CudaError):
+    """An earlier decode through this scratch wrote NaN for a head whose split
+    workgroups did not share an XCD (the XCD-local hand-off's self-check)."""
+    status = 13
+
+
 _BY_STATUS = {c.status: c for c in (UnsupportedAttention, OddCacheCapacity, CacheOverrun, SliceOverrun,
                                     RaggedBlock, MismatchedQ8, OddHeadDim, Driver, NoDevice, InvalidArgument,
-                                    ScratchGrowthInCapture, ScratchLimit)}
+                                    ScratchGrowthInCapture, ScratchLimit, SplitHeadLost)}
 
 
 def _check(status: int):
@@ -141,6 +148,12 @@ class DecodeScratch:
     @property
     def handle(self):
         return self._h
+
+    def check(self):
+        """Raises SplitHeadLost if an earlier decode through this scratch lost
+        a head to the XCD-local check (read after a synchronisation); the
+        status is cleared."""
+        _check(_lib.lib().llmtie_decode_scratch_status(self._h))
 
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None
