@@ -139,7 +139,12 @@ int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint1
 /* ----------------------------------------------------------------- decode */
 
 /* Gpu::attn_decode_f16 (device.rs:5949): one query row [heads*head_dim] over
- * tk live positions of an f16 cache; scale on q (scale_q) or on the scores. */
+ * tk live positions of an f16 cache; scale on q (scale_q) or on the scores.
+ * Every decode entry accepts head_dim 64 and 128 and GQA groups up to 16: a
+ * superset of the reference's refusals (it refuses groups over 4, 8 for its
+ * head_dim-64 g8 kernel, device.rs:6245-6251, and an f32 cache at head_dim
+ * 128, device.rs:6146). A binding that relies on those refusals to choose a
+ * fallback refuses such shapes itself. */
 int llmtie_attn_decode_f16(void* stream, const float* q, size_t q_len, const uint16_t* k, size_t k_len,
                            const uint16_t* v, size_t v_len, size_t heads, size_t kv_heads, size_t head_dim,
                            size_t tk, size_t cap, float scale, int scale_q, llmtie_decode_scratch* scratch,
@@ -173,7 +178,8 @@ int llmtie_attn_decode_f16_q_row(void* stream, const float* q, size_t q_len, siz
                                  llmtie_decode_scratch* scratch, float* out, size_t out_len, int8_t* twin,
                                  size_t twin_rows, size_t twin_k, size_t row);
 
-/* Gpu::attn_decode (device.rs:6132): the same off an f32 cache. */
+/* Gpu::attn_decode (device.rs:6132): the same off an f32 cache (head_dim 128
+ * accepted as well as the reference's 64). */
 int llmtie_attn_decode(void* stream, const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
                        size_t v_len, size_t heads, size_t kv_heads, size_t head_dim, size_t tk, size_t cap,
                        float scale, int scale_q, llmtie_decode_scratch* scratch, float* out, size_t out_len);
