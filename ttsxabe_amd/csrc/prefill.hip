@@ -410,6 +410,24 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
 // one tile that reaches past ktot they are zeroed in LDS before use.
 // W: waves per workgroup, 4, or 8 for the encoder rows (NQT = 1: the tile
 // staging per query row of two query tiles per wave, at two waves per SIMD).
+// Where the staged stacked-rows V tile keeps MFMA operand lane `ln` of dim
+// tile t's fragment (a bijection of the 64 chunks for each t; the fragment
+// read inverts nothing, it reads chunk rows_chunk(lane, t)). Writers put 2 (VR
+// keys x 2 bytes) of a chunk's 16 bytes per lane.
+//   VR = 2: chunk low nibble = 4 ((ln ^ t) & 3) + ((ln >> 2) & 3), i.e. the
+//     two 2-bit fields of ln's low nibble swapped, the dim field XOR t. A
+//     write instruction (fixed dim offset e, so ln & 3 = e) has its lanes at
+//     ln = 4 r + e + 16 K over r, t and four key pairs (the 4-byte word of
+//     the chunk): the chunk's low nibble 4 (e ^ t) + r is distinct over all
+//     (r, t), and its low three bits over (r, t & 1) - the 64 lanes on 64
+//     banks, each 32-lane half on 32.
+//   VR = 4: ln ^ t (the low two bits XOR the dim tile).
+template <int VR>
+__device__ __forceinline__ int rows_chunk(int ln, int t) {
+    if constexpr (VR == 2) return (ln & ~15) | (((ln ^ t) & 3) << 2) | ((ln >> 2) & 3);
+    else return ln ^ (t & 3);
+}
+
 template <int HD, int KIND, int NQT, int W>
 __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(PrefillArgs a) {
     static_assert(W == PW || (W == 8 && KIND == PF_ROWS), "eight waves: encoder rows only");
@@ -491,7 +509,15 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
     constexpr int KI = KF / W;         // staging slots holding K fragments
     constexpr int VR = 1024 / TW;      // rows V: keys per thread (4, or 2 at eight waves)
     static_assert(KIND != PF_ROWS || (HD == 64 && KF % W == 0 && 2 * (NF - KI) == VR), "rows: hd 64");
-    const int rdq = tid & 15, kb = VR * (tid >> 4);  // rows V: dims 4*rdq .. +3, keys kb .. kb + VR - 1
+    // Rows V: thread takes dims 4*rdq .. +3 of keys kb .. kb + VR - 1. At VR
+    // = 2 (eight waves) lane = (rdq & 3) + 4 kp + 16 (rdq >> 2) for key pair
+    // kp: four consecutive lanes read one row's 64 contiguous bytes, and each
+    // 32-lane half of a 4-byte LDS write covers 8 dims x 4 key pairs, which
+    // the chunk swizzle (rows_chunk) puts on 32 distinct banks (64 for the
+    // whole wave). (Key pair fastest, lane = kp + 4 rdq, was as free of bank
+    // conflicts but scattered the row reads: C4 encoder 36.3 vs 34.0 us.)
+    const int rdq = VR == 2 ? (tid & 3) + 4 * ((tid >> 4) & 3) : tid & 15;
+    const int kb = VR == 2 ? VR * (((tid >> 2) & 3) + 4 * (tid >> 6)) : VR * (tid >> 4);
     auto stage_load = [&](auto set_tag, int kv0) __attribute__((always_inline)) {
         constexpr int SS = decltype(set_tag)::value;
         if constexpr (KIND == PF_ROWS) {
@@ -558,11 +584,10 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
 #pragma unroll
                 for (int u = 0; u < VR; ++u) y[u] = to_h(e == 0 ? x[u].x : e == 1 ? x[u].y : e == 2 ? x[u].z : x[u].w);
                 const int frag = KF + (kb >> 5) * NT + (dd >> 4);
-                // Chunk (lane) index XOR the dim tile: a wave's 16 dims of one
-                // instruction land on 16 distinct 16-byte bank slots (unswizzled,
-                // the four dim tiles' chunks share 4 slots). The fragment read
-                // applies the same XOR (rows_lane).
-                const int ln = ((dd & 15) + 16 * ((kb >> 3) & 3)) ^ (dd >> 4);
+                // The MFMA operand lane holding this dim and key group, moved
+                // to the chunk rows_chunk gives it; the fragment read applies
+                // the same map.
+                const int ln = rows_chunk<VR>((dd & 15) + 16 * ((kb >> 3) & 3), dd >> 4);
                 *reinterpret_cast<hv*>(dst + frag * FH + ln * 8 + (kb & 7)) = y;
             }
         }
@@ -754,7 +779,7 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 // Rows: V chunks are swizzled by the dim tile (stage_store).
-                const half8 af = vf[(hf * NT + t) * 64 + (KIND == PF_ROWS ? (lane ^ (t & 3)) : lane)];
+                const half8 af = vf[(hf * NT + t) * 64 + (KIND == PF_ROWS ? rows_chunk<1024 / TW>(lane, t) : lane)];
 #pragma unroll
                 for (int u = 0; u < NQT; ++u) o[t][u] = mfma16(af, pb[hf][u], o[t][u]);
             }
