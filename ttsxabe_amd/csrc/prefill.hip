@@ -428,6 +428,90 @@ __device__ __forceinline__ int rows_chunk(int ln, int t) {
     else return ln ^ (t & 3);
 }
 
+#ifndef LLMTIE_PF_LAZY
+#define LLMTIE_PF_LAZY 1
+#endif
+// The online softmax of query tile u over one 64-key tile, in log2 units:
+// lane (col, grp) holds row 16u + col's scores of keys 32 hf + 8 grp + 4 T + r.
+// P = 2^(score * sl2 - m) is formed against a reference max m that moves
+// only when it must, and O and l carry the same factor 2^-m, so O / l is
+// unchanged by where m sits.
+// Lazy (LLMTIE_PF_LAZY): the probabilities are formed against the current m
+// first; only when some lane's sum exceeds 2^15 (a score more than ~15 above
+// m, or a NaN), or a row has no reference yet, does the wave take the tile's
+// max, move m, rescale O and l and form them again. Between moves every P is
+// at most 2^15, inside f16 at full relative precision, and m never exceeds
+// the row's running max, so no P is smaller than 2^(score - running max).
+// The tile's max (16 maxima and a 4-lane reduction per row) is thus taken
+// only on the rare tiles that move m. Otherwise m moves when the tile's max
+// exceeds it by more than 8, checked on every tile.
+template <bool MASK, int NT, int NQT>
+__device__ __forceinline__ void softmax_tile(floatx4 (&sc)[2][2][NQT], int u, int kv0, int grp, int ilim,
+                                             float sl2, float& m, float& l, floatx4 (&o)[NT][NQT],
+                                             half8 (&pb)[2][NQT]) {
+    if constexpr (MASK) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int T = 0; T < 2; ++T)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = kv0 + 32 * hf + 8 * grp + 4 * T + r;
+                    sc[hf][T][u][r] = key <= ilim ? sc[hf][T][u][r] : ninf();
+                }
+    }
+    auto form = [&]() __attribute__((always_inline)) {
+        // A row whose every key so far is masked keeps m = -inf.
+        const float msub = m == ninf() ? 0.0f : m;
+        float ps = 0.0f;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            half8 p;
+#pragma unroll
+            for (int T = 0; T < 2; ++T)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float e = ex2(__builtin_fmaf(sc[hf][T][u][r], sl2, -msub));
+                    ps += e;
+                    p[4 * T + r] = to_h(e);
+                }
+            pb[hf][u] = p;
+        }
+        return ps;
+    };
+    auto move = [&]() __attribute__((always_inline)) {
+        float mx = ninf();
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int T = 0; T < 2; ++T)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[hf][T][u][r]);
+        mx = max4grp(mx) * sl2;
+        return mx;
+    };
+    auto rescale = [&](float mx) __attribute__((always_inline)) {
+        const float mn = fmaxf(m, mx);
+        const float fac = mn == ninf() ? 1.0f : ex2(m - mn);
+        m = mn;
+        l *= fac;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) o[t][u] *= fac;
+    };
+#if LLMTIE_PF_LAZY
+    float ps = form();
+    if (__any(m == ninf() || !(ps <= 32768.0f))) {
+        rescale(move());
+        ps = form();
+    }
+#else
+    const float mx = move();
+    if (__any(mx > m + 8.0f)) rescale(mx);
+    const float ps = form();
+#endif
+    l += ps;
+}
+
 template <int HD, int KIND, int NQT, int W>
 __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(PrefillArgs a) {
     static_assert(W == PW || (W == 8 && KIND == PF_ROWS), "eight waves: encoder rows only");
@@ -685,7 +769,6 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
         ilim[u] = a.causal ? min(a.past + r, ktot - 1) : ktot - 1;
     }
     const float sl2 = (a.scale_q ? 1.0f : a.scale) * LLMTIE_LOG2E;
-    constexpr float RB = 8.0f;  // log2 headroom before the reference max moves
 
     // One 64-key tile from LDS buffer `tb`; MASK: some key of it lies past
     // some row's limit.
@@ -727,52 +810,7 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
         __builtin_amdgcn_sched_barrier(0);
         half8 pb[2][NQT];
 #pragma unroll
-        for (int u = 0; u < NQT; ++u) {
-            // The reference max m is kept in log2 units and only moves when a
-            // tile's max exceeds it by more than RB (rare after the first
-            // tiles), so O and l are rescaled rarely; in between the
-            // probabilities 2^(score * sl2 - m) are at most 2^RB, well inside
-            // f16, and O / l is unchanged (both carry the same 2^-m).
-            float mx = ninf();
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-                for (int T = 0; T < 2; ++T)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if constexpr (MASK) {
-                            const int key = kv0 + 32 * hf + 8 * grp + 4 * T + r;
-                            sc[hf][T][u][r] = key <= ilim[u] ? sc[hf][T][u][r] : ninf();
-                        }
-                        mx = fmaxf(mx, sc[hf][T][u][r]);
-                    }
-            mx = max4grp(mx) * sl2;
-            if (__any(mx > m[u] + RB)) {
-                const float mn = fmaxf(m[u], mx);
-                // A row whose every key so far is masked keeps m = -inf.
-                const float fac = mn == ninf() ? 1.0f : ex2(m[u] - mn);
-                m[u] = mn;
-                l[u] *= fac;
-#pragma unroll
-                for (int t = 0; t < NT; ++t) o[t][u] *= fac;
-            }
-            const float msub = m[u] == ninf() ? 0.0f : m[u];
-            float ps = 0.0f;
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                half8 p;
-#pragma unroll
-                for (int T = 0; T < 2; ++T)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float e = ex2(__builtin_fmaf(sc[hf][T][u][r], sl2, -msub));
-                        ps += e;
-                        p[4 * T + r] = to_h(e);
-                    }
-                pb[hf][u] = p;
-            }
-            l[u] += ps;
-        }
+        for (int u = 0; u < NQT; ++u) softmax_tile<MASK>(sc, u, kv0, grp, ilim[u], sl2, m[u], l[u], o, pb);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
@@ -1027,7 +1065,6 @@ __global__ __launch_bounds__(PPW * LLMTIE_WAVE, 1) void flash_pp_kernel(PrefillA
         ilim[u] = a.causal ? min(a.past + r, ktot - 1) : ktot - 1;
     }
     const float sl2 = (a.scale_q ? 1.0f : a.scale) * LLMTIE_LOG2E;
-    constexpr float RB = 8.0f;
     floatx4 sc[2][2][NQT];
     half8 pb2[2][NQT];
 
@@ -1090,46 +1127,7 @@ __global__ __launch_bounds__(PPW * LLMTIE_WAVE, 1) void flash_pp_kernel(PrefillA
     auto softmax = [&](int kv0, auto mask_tag) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
-        for (int u = 0; u < NQT; ++u) {
-            float mx = ninf();
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-                for (int T = 0; T < 2; ++T)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if constexpr (MASK) {
-                            const int key = kv0 + 32 * hf + 8 * grp + 4 * T + r;
-                            sc[hf][T][u][r] = key <= ilim[u] ? sc[hf][T][u][r] : ninf();
-                        }
-                        mx = fmaxf(mx, sc[hf][T][u][r]);
-                    }
-            mx = max4grp(mx) * sl2;
-            if (__any(mx > m[u] + RB)) {
-                const float mn = fmaxf(m[u], mx);
-                const float fac = mn == ninf() ? 1.0f : ex2(m[u] - mn);
-                m[u] = mn;
-                l[u] *= fac;
-#pragma unroll
-                for (int t = 0; t < NT; ++t) o[t][u] *= fac;
-            }
-            const float msub = m[u] == ninf() ? 0.0f : m[u];
-            float ps = 0.0f;
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                half8 p;
-#pragma unroll
-                for (int T = 0; T < 2; ++T)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float e = ex2(__builtin_fmaf(sc[hf][T][u][r], sl2, -msub));
-                        ps += e;
-                        p[4 * T + r] = to_h(e);
-                    }
-                pb2[hf][u] = p;
-            }
-            l[u] += ps;
-        }
+        for (int u = 0; u < NQT; ++u) softmax_tile<MASK>(sc, u, kv0, grp, ilim[u], sl2, m[u], l[u], o, pb2);
     };
 
     if (ntile > 0) {
