@@ -428,23 +428,22 @@ __device__ __forceinline__ int rows_chunk(int ln, int t) {
     else return ln ^ (t & 3);
 }
 
-#ifndef LLMTIE_PF_LAZY
-#define LLMTIE_PF_LAZY 1
-#endif
+// A row's reference max before it has one: finite, so P = 2^(score * sl2 -
+// m) of any live key overflows to +inf (and moves m), while masked keys
+// (-inf) still give 0 and a row with no live key yet keeps it.
+constexpr float PF_NOREF = -1e30f;
 // The online softmax of query tile u over one 64-key tile, in log2 units:
 // lane (col, grp) holds row 16u + col's scores of keys 32 hf + 8 grp + 4 T + r.
 // P = 2^(score * sl2 - m) is formed against a reference max m that moves
-// only when it must, and O and l carry the same factor 2^-m, so O / l is
-// unchanged by where m sits.
-// Lazy (LLMTIE_PF_LAZY): the probabilities are formed against the current m
-// first; only when some lane's sum exceeds 2^15 (a score more than ~15 above
-// m, or a NaN), or a row has no reference yet, does the wave take the tile's
-// max, move m, rescale O and l and form them again. Between moves every P is
-// at most 2^15, inside f16 at full relative precision, and m never exceeds
-// the row's running max, so no P is smaller than 2^(score - running max).
-// The tile's max (16 maxima and a 4-lane reduction per row) is thus taken
-// only on the rare tiles that move m. Otherwise m moves when the tile's max
-// exceeds it by more than 8, checked on every tile.
+// only when it must; O and l carry the same factor 2^-m, so O / l does not
+// depend on where m sits. The probabilities are formed against the current
+// m first; only when some lane's sum exceeds 2^15 (a score more than ~15
+// above m, a row's first live key, or a NaN) does the wave take the tile's
+// max, move m, rescale O and l and form them again. So every P is at most
+// 2^15, inside f16 at full relative precision, m never exceeds the row's
+// running max (no P is smaller than 2^(score - running max)), and the
+// tile's max (16 maxima and a 4-lane reduction per row) is taken only on the
+// rare tiles that move m.
 template <bool MASK, int NT, int NQT>
 __device__ __forceinline__ void softmax_tile(floatx4 (&sc)[2][2][NQT], int u, int kv0, int grp, int ilim,
                                              float sl2, float& m, float& l, floatx4 (&o)[NT][NQT],
@@ -461,8 +460,6 @@ __device__ __forceinline__ void softmax_tile(floatx4 (&sc)[2][2][NQT], int u, in
                 }
     }
     auto form = [&]() __attribute__((always_inline)) {
-        // A row whose every key so far is masked keeps m = -inf.
-        const float msub = m == ninf() ? 0.0f : m;
         float ps = 0.0f;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
@@ -471,15 +468,16 @@ __device__ __forceinline__ void softmax_tile(floatx4 (&sc)[2][2][NQT], int u, in
             for (int T = 0; T < 2; ++T)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float e = ex2(__builtin_fmaf(sc[hf][T][u][r], sl2, -msub));
-                    ps += e;
+                    const float e = ex2(__builtin_fmaf(sc[hf][T][u][r], sl2, -m));
+                    ps = (hf | T | r) ? ps + e : e;
                     p[4 * T + r] = to_h(e);
                 }
             pb[hf][u] = p;
         }
         return ps;
     };
-    auto move = [&]() __attribute__((always_inline)) {
+    float ps = form();
+    if (__any(!(ps <= 32768.0f))) {
         float mx = ninf();
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
@@ -487,28 +485,14 @@ __device__ __forceinline__ void softmax_tile(floatx4 (&sc)[2][2][NQT], int u, in
             for (int T = 0; T < 2; ++T)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[hf][T][u][r]);
-        mx = max4grp(mx) * sl2;
-        return mx;
-    };
-    auto rescale = [&](float mx) __attribute__((always_inline)) {
-        const float mn = fmaxf(m, mx);
-        const float fac = mn == ninf() ? 1.0f : ex2(m - mn);
+        const float mn = fmaxf(m, max4grp(mx) * sl2);
+        const float fac = ex2(m - mn);
         m = mn;
         l *= fac;
 #pragma unroll
         for (int t = 0; t < NT; ++t) o[t][u] *= fac;
-    };
-#if LLMTIE_PF_LAZY
-    float ps = form();
-    if (__any(m == ninf() || !(ps <= 32768.0f))) {
-        rescale(move());
         ps = form();
     }
-#else
-    const float mx = move();
-    if (__any(mx > m + 8.0f)) rescale(mx);
-    const float ps = form();
-#endif
     l += ps;
 }
 
@@ -659,8 +643,14 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
             typedef _Float16 hv __attribute__((ext_vector_type(VR)));
             float4 x[VR];
 #pragma unroll
-            for (int u = 0; u < VR; ++u)
-                x[u] = kv0 + kb + u < ktot ? sr[SS][KI + u / 2][u % 2] : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int u = 0; u < VR; ++u) x[u] = sr[SS][KI + u / 2][u % 2];
+            // Only the tile reaching past the keys has V rows to zero: a
+            // wave-uniform branch, so full tiles convert with no per-key select.
+            if (kv0 + KT > ktot) {
+#pragma unroll
+                for (int u = 0; u < VR; ++u)
+                    if (kv0 + kb + u >= ktot) x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int dd = 4 * rdq + e;
@@ -763,7 +753,7 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
     int ilim[NQT];
 #pragma unroll
     for (int u = 0; u < NQT; ++u) {
-        m[u] = ninf();
+        m[u] = PF_NOREF;
         l[u] = 0.0f;
         const int r = p0 + 16 * u + col;
         ilim[u] = a.causal ? min(a.past + r, ktot - 1) : ktot - 1;
@@ -1059,7 +1049,7 @@ __global__ __launch_bounds__(PPW * LLMTIE_WAVE, 1) void flash_pp_kernel(PrefillA
     int ilim[NQT];
 #pragma unroll
     for (int u = 0; u < NQT; ++u) {
-        m[u] = ninf();
+        m[u] = PF_NOREF;
         l[u] = 0.0f;
         const int r = p0 + 16 * u + col;
         ilim[u] = a.causal ? min(a.past + r, ktot - 1) : ktot - 1;
