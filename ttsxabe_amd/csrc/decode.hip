@@ -1192,10 +1192,12 @@ __global__ __launch_bounds__(DT) void attn_merge_kernel(DecodeArgs a) {
 //
 // Every (sequence, kv head, 32-key block) of the batch is one position of a
 // flat list, sequence-major, then kv head, then block; the launch's waves
-// each take an equal contiguous range of it, so every wave streams the same
-// number of blocks whatever the spread of the sequences' lengths (a
-// per-head split of a fixed span leaves the last, short split of each head
-// idle for most of the launch). A wave walks its range with the two-deep
+// each take a contiguous range of it of equal cost (its blocks, plus one
+// block's worth for each kv head starting in it: a segment's start and end
+// cost a wave about a block's time), so every wave streams about the same
+// work whatever the spread of the sequences' lengths (a per-head split of a
+// fixed span leaves the last, short split of each head idle for most of the
+// launch). A wave walks its range with the two-deep
 // block prefetch of attn_decode_kernel; the range falls into segments, one
 // per kv head it touches:
 //   - a segment that is a whole head: the wave normalises and writes the
@@ -1222,12 +1224,6 @@ __device__ __forceinline__ long rdfirst64(long v) {
     return (long)(((unsigned long)hi << 32) | lo);
 }
 
-// Waves of the launch that take part (never more than there are blocks, so
-// every wave's range is non-empty), and wave u's range [first(u), first(u+1)).
-__device__ __forceinline__ long sk_first(long u, long nw, long total) { return u * total / nw; }
-// The wave whose range holds position p.
-__device__ __forceinline__ long sk_owner(long p, long nw, long total) { return ((p + 1) * nw - 1) / total; }
-
 // The batch's sequences, one per lane (nseq <= 64): blocks per kv head and
 // the position of the sequence's first block in the flat list.
 struct SkSeqs {
@@ -1235,6 +1231,9 @@ struct SkSeqs {
     int tk, slot;
     long base;   // flat position of (this sequence, kv head 0, block 0)
     long total;  // positions in the whole batch (wave-uniform)
+    long vbase;  // the same in cost units (see sk_first)
+    long vend;   // vbase of the next sequence
+    long vtotal; // cost units of the whole batch (wave-uniform)
 };
 __device__ __forceinline__ SkSeqs sk_seqs(const DecodeArgs& a, int lane) {
     SkSeqs q;
@@ -1255,7 +1254,46 @@ __device__ __forceinline__ SkSeqs sk_seqs(const DecodeArgs& a, int lane) {
     }
     q.base = incl - cnt;
     q.total = rdlane64(incl, 63);
+    // Cost units: a kv head costs its blocks plus one for the segment that
+    // starts at it (its queries converted, a context written or a partial
+    // stashed: about one block's time in a wave's stream).
+    const long vcnt = q.nb > 0 ? (long)(q.nb + 1) * a.kv_heads : 0;
+    long vincl = vcnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const long y = __shfl_up(vincl, o, 64);
+        if (lane >= o) vincl += y;
+    }
+    q.vbase = vincl - vcnt;
+    q.vend = vincl;
+    q.vtotal = rdlane64(vincl, 63);
     return q;
+}
+
+// The partition of the flat block list over the nw waves that take part
+// (nw <= total), balanced in cost units: each kv head is one unit (its
+// start) followed by its blocks, and wave u takes the blocks whose units
+// lie in [u V / nw, (u + 1) V / nw), V = vtotal. Wave u's range of blocks is
+// [sk_first(u), sk_first(u + 1)); it is empty when its units hold only a
+// head's start.
+__device__ __forceinline__ long sk_first(const SkSeqs& q, long u, long nw) {
+    const long x = u * q.vtotal / nw;
+    if (x >= q.vtotal) return q.total;
+    // The sequence holding unit x: those ending at or before it are a
+    // prefix of the lanes (lanes past the batch end at V > x).
+    const int s = __popcll(__ballot(q.vend <= x));
+    const int nb = rdlane(q.nb, s);
+    const long xo = x - rdlane64(q.vbase, s);
+    const long h = xo / (nb + 1), j = xo % (nb + 1);
+    return rdlane64(q.base, s) + h * nb + (j > 0 ? j - 1 : 0);
+}
+// The wave whose range holds block p.
+__device__ __forceinline__ long sk_owner(const SkSeqs& q, long p, int kv_heads, long nw) {
+    const int s = __popcll(__ballot(q.base + (long)q.nb * kv_heads <= p));
+    const int nb = rdlane(q.nb, s);
+    const long off = p - rdlane64(q.base, s);
+    const long v = rdlane64(q.vbase, s) + off + off / nb + 1;
+    return ((v + 1) * nw - 1) / q.vtotal;
 }
 
 // Where flat position p lies: sequence, kv head, block (all wave-uniform).
@@ -1431,7 +1469,8 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
         }
     }
     if (u >= nw) return;
-    const long p_first = sk_first(u, nw, total), p_end = sk_first(u + 1, nw, total);
+    const long p_first = sk_first(sq, u, nw), p_end = sk_first(sq, u + 1, nw);
+    if (p_first >= p_end) return;  // units holding only a head's start
     const long nblk_cap = tiled_nblk(a.cap);
 
     // The next block to issue, as a cursor stepping through the list
@@ -1645,12 +1684,12 @@ __global__ __launch_bounds__(DT, 1) void attn_decode_sk_kernel(DecodeArgs a) {
         const SkPos r = sk_locate(sq, hs, kv);
         const long he = hs + r.nb;
         Head h;
-        h.c0 = sk_owner(hs, nw, total);
-        h.c1 = sk_owner(he - 1, nw, total);
+        h.c0 = sk_owner(sq, hs, kv, nw);
+        h.c1 = sk_owner(sq, he - 1, kv, nw);
         // Every contributor but the last publishes the head as the segment
         // ending its range (slot 1); the last one, as slot 1 only if its
         // range ends with the head.
-        h.last_sl = sk_first(h.c1 + 1, nw, total) == he ? 1 : 0;
+        h.last_sl = sk_first(sq, h.c1 + 1, nw) == he ? 1 : 0;
         h.idx = r.s * kv + r.h;
         h.c0 = rdfirst64(h.c0);
         h.c1 = rdfirst64(h.c1);
