@@ -66,6 +66,50 @@ def test_fused_attention_holds_at_the_prefill_shapes(gpu, args):
     fused_attention_sized(gpu, *args)
 
 
+@pytest.mark.parametrize("causal,tiled,start", [(True, True, 0.0), (False, False, 0.0), (True, False, -60.0),
+                                                 (False, True, -60.0)])
+def test_the_reference_max_moves_across_tiles(gpu, causal, tiled, start):
+    """Scores that climb by ~45 (log2 units) every 64-key tile, from -75, or
+    from start - 75 (every score of the first tiles far below zero), so the
+    softmax's reference max must move on nearly every tile and a row's first
+    live keys must set it (a reference of zero would flush their f16
+    probabilities to nothing); against the reference's f64 prefill and rule
+    (kernels.rs:2290-2374)."""
+    from ttsxabe_amd.gpu import TiledCache16
+    heads, kv, hd, tq, past, cap = 4, 2, 64, 200, 0, 256
+    tk = past + tq
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    rng = np.random.default_rng(7)
+    # Query row r: 40 along dim 0 (plus noise); key j: (j - 100) / 10 along
+    # dim 0, so the score of key j is ~ (j - 100) / 2 + start, rising ~32
+    # (natural units) a tile.
+    q = (rng.standard_normal((tq, heads, hd)) * 0.1).astype(np.float32)
+    q[:, :, 0] = 40.0
+    q[:, :, 1] = start * 8.0 / 3.0 if start else 0.0
+    kk = (rng.standard_normal((kv, tk, hd)) * 0.1).astype(np.float32)
+    kk[:, :, 0] = (np.arange(tk) - 100) / 10.0
+    kk[:, :, 1] = 3.0 if start else kk[:, :, 1]
+    vv = rng.standard_normal((kv, tk, hd)).astype(np.float32)
+    kk = kk.astype(np.float16).astype(np.float32)  # f16-exact, so the oracle sees the cache's values
+    vv = vv.astype(np.float16).astype(np.float32)
+    kc, vc = caches(kk.reshape(-1), vv.reshape(-1), kv, tk, cap, hd)
+    q = q.reshape(-1)
+    if tiled:
+        t = TiledCache16(kv, hd, cap, zero=False)
+        t.data.fill_(float("nan"))
+        gpu.t16_from_ref(up_f16(kc), up_f16(vc), t, tk)
+        out = gpu.flash_attn_t16(up(q), t, tq, past, heads, scale, causal)
+    else:
+        out = gpu.flash_attn_f16(up(q), up_f16(kc), up_f16(vc), tq, past, heads, kv, hd, cap, scale, causal)
+    got = down(out).astype(np.float64)
+    want, spread = oracle.prefill_ref(q, heads * hd, kc, vc, tq, past, heads, kv, hd, cap, scale, causal)
+    tol = 2e-4 + 1e-2 * np.abs(want) + 1e-2 * spread
+    err = np.abs(want - got)
+    assert np.isfinite(got).all()
+    assert (err <= tol).all(), f"worst {float((err / tol).max())} of tolerance"
+    assert float((err / tol).max()) < 0.5
+
+
 def test_an_uninstantiated_head_width_is_refused(gpu):
     from ttsxabe_amd.gpu import UnsupportedAttention
     assert not gpu.supports_flash(96, 4, 4)
