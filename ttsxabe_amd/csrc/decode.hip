@@ -1358,9 +1358,9 @@ __device__ __forceinline__ void ring_read<128>(uint32_t b, int lane, int grp, Fr
         "ds_read_b128 %14, %17 offset:384\n"
         "ds_read_b128 %15, %17 offset:448\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=v"(f.kc[0][0]), "=v"(f.kc[0][1]), "=v"(f.kc[1][0]), "=v"(f.kc[1][1]), "=v"(f.vc[0]), "=v"(f.vc[1]),
-          "=v"(f.vc[2]), "=v"(f.vc[3]), "=v"(f.ks[0]), "=v"(f.ks[1]), "=v"(f.ks[2]), "=v"(f.ks[3]), "=v"(f.vs[0]),
-          "=v"(f.vs[1]), "=v"(f.vs[2]), "=v"(f.vs[3])
+        : "=&v"(f.kc[0][0]), "=&v"(f.kc[0][1]), "=&v"(f.kc[1][0]), "=&v"(f.kc[1][1]), "=&v"(f.vc[0]), "=&v"(f.vc[1]),
+          "=&v"(f.vc[2]), "=&v"(f.vc[3]), "=&v"(f.ks[0]), "=&v"(f.ks[1]), "=&v"(f.ks[2]), "=&v"(f.ks[3]), "=&v"(f.vs[0]),
+          "=&v"(f.vs[1]), "=&v"(f.vs[2]), "=&v"(f.vs[3])
         : "v"(c), "v"(sc));
 }
 template <>
@@ -1378,14 +1378,17 @@ __device__ __forceinline__ void ring_read<64>(uint32_t b, int lane, int grp, Fra
         "ds_read_b128 %6, %9 offset:128\n"
         "ds_read_b128 %7, %9 offset:192\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=v"(f.kc[0][0]), "=v"(f.kc[1][0]), "=v"(f.vc[0]), "=v"(f.vc[1]), "=v"(f.ks[0]), "=v"(f.ks[1]),
-          "=v"(f.vs[0]), "=v"(f.vs[1])
+        : "=&v"(f.kc[0][0]), "=&v"(f.kc[1][0]), "=&v"(f.vc[0]), "=&v"(f.vc[1]), "=&v"(f.ks[0]), "=&v"(f.ks[1]),
+          "=&v"(f.vs[0]), "=&v"(f.vs[1])
         : "v"(c), "v"(sc));
 }
 
 // A lane's query operands from a raw [g][HD] f32 buffer in LDS (b = the
 // byte address of its column's dims 8*grp ..): dims 32s + 8grp + 0..7 as
-// two float4 per s, read as one asm block (see ring_read).
+// two float4 per s, read as one asm block (see ring_read). Every output of
+// these multi-read blocks is early-clobber ("=&v"): the reads are issued
+// back to back, so an output sharing a register with the address would be
+// overwritten by one read's return while a later read still needs it.
 template <int HD>
 __device__ __forceinline__ void q_read(uint32_t b, float4 (&x)[HD / 32][2]);
 template <>
@@ -1400,8 +1403,8 @@ __device__ __forceinline__ void q_read<128>(uint32_t b, float4 (&x)[4][2]) {
         "ds_read_b128 %6, %8 offset:384\n"
         "ds_read_b128 %7, %8 offset:400\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=v"(x[0][0]), "=v"(x[0][1]), "=v"(x[1][0]), "=v"(x[1][1]), "=v"(x[2][0]), "=v"(x[2][1]), "=v"(x[3][0]),
-          "=v"(x[3][1])
+        : "=&v"(x[0][0]), "=&v"(x[0][1]), "=&v"(x[1][0]), "=&v"(x[1][1]), "=&v"(x[2][0]), "=&v"(x[2][1]), "=&v"(x[3][0]),
+          "=&v"(x[3][1])
         : "v"(b));
 }
 template <>
@@ -1412,7 +1415,7 @@ __device__ __forceinline__ void q_read<64>(uint32_t b, float4 (&x)[2][2]) {
         "ds_read_b128 %2, %4 offset:128\n"
         "ds_read_b128 %3, %4 offset:144\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=v"(x[0][0]), "=v"(x[0][1]), "=v"(x[1][0]), "=v"(x[1][1])
+        : "=&v"(x[0][0]), "=&v"(x[0][1]), "=&v"(x[1][0]), "=&v"(x[1][1])
         : "v"(b));
 }
 
