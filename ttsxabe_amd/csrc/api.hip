@@ -147,6 +147,8 @@ int llmtie_supports_flash(size_t head_dim, size_t heads, size_t kv_heads) {
 
 namespace {
 
+int compute_units();
+
 // 16-query tiles per wave: the most that still leaves about two workgroups
 // per CU (256 CUs), so short prefills spread over the whole chip.
 int pick_nqt(size_t tq, size_t heads, int gb, bool staged = false) {
@@ -186,6 +188,7 @@ int prefill_common(void* stream, int kind, const float* q, size_t q_len, const v
     const size_t group = heads / kv_heads;
     const int gb = group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
     PrefillArgs a{};
+    a.cus = compute_units();
     a.q = q;
     a.k = k;
     a.v = v;
@@ -502,6 +505,7 @@ int llmtie_flash_attn_rows(void* stream, const float* qkv, size_t qkv_len, uint1
     if (t == 0) return ok();
     if (!qkv || !out) return invalid("a buffer");
     PrefillArgs a{};
+    a.cus = compute_units();
     a.q = qkv;
     a.k = qkv + d;
     a.v = qkv + 2 * d;

@@ -36,6 +36,8 @@ struct PrefillArgs {
     // rows: 767 -> 679 us).
     int xcd, nrb;
     int grid8;  // workgroups of the 1-D launch / 8 (read with the arguments, not from the dispatch packet)
+    int cus;          // compute units of the device (set by the entry point)
+    int light_tiles;  // fast f16 kernel, set by launch_prefill: blocks of at most this many tiles wait first (0: none)
 };
 
 // nqt: 16-query tiles per wave (1, 2 or 4). waves: 4, or 8 for the encoder

@@ -44,6 +44,9 @@
 #ifndef LLMTIE_PF_SPD
 #define LLMTIE_PF_SPD 2
 #endif
+#ifndef LLMTIE_PF_SLEEP
+#define LLMTIE_PF_SLEEP 27  // s_sleep units (64 clocks)
+#endif
 #ifndef LLMTIE_PF_PD
 #define LLMTIE_PF_PD 10
 #endif
@@ -716,6 +719,11 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
         // no branch leaves the compiler unsure how many loads are pending.
         if (kend > 0) static_for<SPD>([&](auto i) { stage_load(i, decltype(i)::value * KT); });
     } else {
+        // A causal launch of at most one workgroup per compute unit is as
+        // long as its heaviest blocks' tile chain: the light blocks (at most
+        // half the heaviest's tiles) hold their first loads back ~0.85 us so
+        // the heavy blocks' queries and first tiles meet less traffic.
+        if (a.light_tiles > 0 && (kend + KT - 1) / KT <= a.light_tiles) __builtin_amdgcn_s_sleep(LLMTIE_PF_SLEEP);
         if (kend > 0) issue(0, t0);
     }
     const float qsc = a.scale_q ? a.scale : 1.0f;
@@ -1231,6 +1239,8 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
         const unsigned items = grid.x * grid.y;
         b.xcd = items % 8 == 0 && !(getenv("LLMTIE_PREFILL_XCD") && !atoi(getenv("LLMTIE_PREFILL_XCD")));
         b.grid8 = (int)(items / 8);
+        const int heavy = (a.past + a.tq + KT - 1) / KT;
+        b.light_tiles = a.causal && !w8 && (int)items <= a.cus && heavy >= 6 && LLMTIE_PF_SLEEP > 0 ? heavy / 2 : 0;
         const dim3 g = b.xcd ? dim3(items) : grid;
         if (w8) {
             hipLaunchKernelGGL((flash_fwd_kernel<64, PF_ROWS, 1, 8>), g, block, 0, st, b);
