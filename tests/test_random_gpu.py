@@ -30,7 +30,7 @@ def draw(seed):
     return rng, heads, kv, hd
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_random_f16_decode(gpu, seed):
     from ttsxabe_amd.gpu import DecodeScratch, TiledCache16
     rng, heads, kv, hd = draw(1000 + seed)
@@ -54,7 +54,7 @@ def test_random_f16_decode(gpu, seed):
     assert err < 2e-5, f"{(heads, kv, hd, tk, cap, scale_q)}: {err:.3e} of full scale"
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_random_q8_batch_decode(gpu, seed):
     rng, heads, kv, hd = draw(5000 + seed)
     if heads // kv > 16:
@@ -67,7 +67,7 @@ def test_random_q8_batch_decode(gpu, seed):
     check_batch(gpu, hd, heads, kv, slots, cap, tk, slot, 6000 + seed, scale_q=bool(rng.integers(2)))
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_random_prefill(gpu, seed):
     rng, heads, kv, hd = draw(7000 + seed)
     causal = bool(rng.integers(2))
