@@ -44,6 +44,10 @@ CASES = [
     # group 4 on the MFMA path with one block in flight per wave.
     (4, 4, 128, 300, 320, False, True),
     (8, 2, 128, 1000, 1024, False, False),
+    # f32 caches at head_dim 64, group 1 (line-order fold) with capacity 2 mod
+    # 4: V rows only 8-byte aligned; full blocks and a 14-key partial one.
+    (5, 5, 64, 302, 450, False, False),
+    (3, 3, 64, 450, 450, False, True),
 ]
 
 

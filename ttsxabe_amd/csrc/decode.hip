@@ -738,6 +738,128 @@ __device__ __forceinline__ void load_block_f32v(const Ctx& c, int p0, int lane, 
     }
 }
 
+// The f32 cache at head_dim 64 in line order. The fragment order above has
+// each load instruction touch 16 keys (or 16 V rows) in sixteen 128-byte
+// lines, half of each; a workgroup of a launch that occupies few CUs is then
+// bound by its CU's line rate, not by HBM. Here every instruction reads eight
+// whole lines (1 KB), and the fold is arranged around that:
+//   K: instruction i holds keys 4i + lane/16, dims 4 (lane%16) .. +3, so a
+//      lane's query slice is 4 dims and a key's dot product is spread over
+//      the 16 lanes of a DPP row;
+//   V: instruction i holds rows (dims) 8i + lane/8, keys 4 (lane%8) .. +3.
+template <int HD>
+struct FragF32L {
+    static_assert(HD == 64, "line-order f32 fold: head_dim 64");
+    float4 k[8];
+    float4 v[8];
+};
+
+template <int HD, int VA, bool FULL>
+__device__ __forceinline__ void load_block_f32l(const Ctx& c, int p0, int lane, FragF32L<HD>& f) {
+    const float* kb = reinterpret_cast<const float*>(c.k);
+    const float* vb = reinterpret_cast<const float*>(c.v);
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int key = p0 + 4 * i + (lane >> 4);
+        const bool ok = FULL || key < c.tk;
+        const float4 x = *reinterpret_cast<const float4*>(kb + (size_t)(ok ? key : 0) * HD + 4 * (lane & 15));
+        f.k[i] = ok ? x : z;
+    }
+    const int k0 = p0 + 4 * (lane & 7);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float* r = vb + (size_t)(8 * i + (lane >> 3)) * c.cap + k0;
+        if constexpr (FULL && VA == 16) {
+            f.v[i] = *reinterpret_cast<const float4*>(r);
+        } else if constexpr (FULL) {
+            const float2 a0 = reinterpret_cast<const float2*>(r)[0], a1 = reinterpret_cast<const float2*>(r)[1];
+            f.v[i] = make_float4(a0.x, a0.y, a1.x, a1.y);
+        } else {
+            float x[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x[j] = k0 + j < c.tk ? r[j] : 0.0f;
+            f.v[i] = make_float4(x[0], x[1], x[2], x[3]);
+        }
+    }
+}
+
+// One step of a reduce-scatter across a lane pair that differs in bit B of
+// the lane id (DPP control CTRL selects the partner): of the 2n values, the
+// lane keeps the upper n when its bit B is set, the lower n otherwise, and
+// adds the partner's copies of the same n. Partners keep opposite halves.
+template <int CTRL, int B, int N>
+__device__ __forceinline__ void rs_step(const float (&x)[2 * N], float (&y)[N], int lane) {
+    const bool up = (lane >> B) & 1;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const float keep = up ? x[N + k] : x[k];
+        const float send = up ? x[k] : x[N + k];
+        y[k] = keep + dpp_f<CTRL>(send);
+    }
+}
+
+// One 32-key block of the line-order f32 cache folded into the wave's
+// running (m, l, o). qv: the lane's query dims 4 (lane%16) .. +3 in log2-score
+// units; o[i]: the lane's context sum for dim 8i + lane/8 over keys
+// 4 (lane%8) .. +3 of every block; pw: the wave's 32-float LDS row.
+template <int HD, bool MASK>
+__device__ __forceinline__ void fold_block_g1l(const FragF32L<HD>& f, const float (&qv)[4], int p0, int tk,
+                                               int lane, float& m_run, float& l_run, float (&o)[8], float* pw) {
+    float d[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float acc = f.k[i].x * qv[0];
+        acc = __builtin_fmaf(f.k[i].y, qv[1], acc);
+        acc = __builtin_fmaf(f.k[i].z, qv[2], acc);
+        d[i] = __builtin_fmaf(f.k[i].w, qv[3], acc);
+    }
+    // Sum each key's 16 partial dots over its DPP row: row mirror (bit 3),
+    // half-row mirror (bit 2), quad xor 3 (bit 1) scatter the eight keys,
+    // quad xor 1 completes the pair. Lane ends with key 4 ((lane/2)%8) + lane/16,
+    // as does its xor-1 partner.
+    float d4[4], d2[2], d1[1];
+    rs_step<0x140, 3, 4>(d, d4, lane);
+    rs_step<0x141, 2, 2>(d4, d2, lane);
+    rs_step<0x1b, 1, 1>(d2, d1, lane);
+    float sc = d1[0] + dpp_f<0xb1>(d1[0]);
+    const int kl = 4 * ((lane >> 1) & 7) + (lane >> 4);
+    if constexpr (MASK) sc = p0 + kl < tk ? sc : ninf();
+    const float mn = fmaxf(m_run, wave_max(sc));
+    const float fac = ex2(m_run - mn);
+    m_run = mn;
+    const float e = ex2(sc - mn);
+    // Each key's probability sits in two lanes: half the wave sum is the
+    // block's (an exact scaling).
+    l_run = l_run * fac + wave_sum(e) * 0.5f;
+    if (__any(fac != 1.0f)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] *= fac;
+    }
+    if (!(lane & 1)) pw[kl] = e;
+    __builtin_amdgcn_wave_barrier();
+    const float4 pp = *reinterpret_cast<const float4*>(pw + 4 * (lane & 7));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float acc = __builtin_fmaf(pp.x, f.v[i].x, o[i]);
+        acc = __builtin_fmaf(pp.y, f.v[i].y, acc);
+        acc = __builtin_fmaf(pp.z, f.v[i].z, acc);
+        o[i] = __builtin_fmaf(pp.w, f.v[i].w, acc);
+    }
+    __builtin_amdgcn_wave_barrier();  // the row is read before the next block's writes
+}
+
+// The line-order context sums reduced over the eight lanes that share a dim
+// row: lane ends with dim 8 (lane%8) + lane/8 (half-row mirror, quad xor 3,
+// quad xor 1 scatter the eight dims).
+__device__ __forceinline__ float g1l_context(const float (&o)[8], int lane) {
+    float o4[4], o2[2], o1[1];
+    rs_step<0x141, 2, 4>(o, o4, lane);
+    rs_step<0x1b, 1, 2>(o4, o2, lane);
+    rs_step<0xb1, 0, 1>(o2, o1, lane);
+    return o1[0];
+}
+
 // Element j of a lane's 8-element K or V run, as f32.
 template <int HD, int KIND, typename FR>
 __device__ __forceinline__ float g1_k(const FR& f, int T, int s, int j) {
@@ -844,7 +966,10 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     __shared__ int last;
     __shared__ __attribute__((aligned(16))) float prow[DW][32];  // G1: a block's probabilities
     static_assert(!G1 || KIND != KV_TQ8, "the Q8_0 cache decodes through the MFMA path");
-    using FR = std::conditional_t<G1 && KIND == KV_F32, FragF32<HD>, Frag<HD, KIND>>;
+    // G1L: the f32 cache at head_dim 64 in line order (FragF32L).
+    constexpr bool G1L = G1 && KIND == KV_F32 && HD == 64;
+    using FR = std::conditional_t<G1L, FragF32L<HD>,
+                                  std::conditional_t<G1 && KIND == KV_F32, FragF32<HD>, Frag<HD, KIND>>>;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -898,7 +1023,8 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     FR f0, f1;
     auto ld = [&](int p, FR& f, auto full_tag) __attribute__((always_inline)) {
         constexpr bool FULL = decltype(full_tag)::value;
-        if constexpr (G1 && KIND == KV_F32) load_block_f32v<HD, VA, FULL>(c, p, lane, f);
+        if constexpr (G1L) load_block_f32l<HD, VA, FULL>(c, p, lane, f);
+        else if constexpr (G1 && KIND == KV_F32) load_block_f32v<HD, VA, FULL>(c, p, lane, f);
         else load_block<HD, KIND, VA, FULL, !G1>(c, p, lane, f);
     };
     // The first two blocks go out before the queries are read: the queries'
@@ -914,16 +1040,25 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     const float* q = a.q + a.q_off + (size_t)seq * a.q_stride + ((size_t)h * group) * HD;
     const bool qok = col < group;
     const float* qc = q + (size_t)(qok ? col : 0) * HD + 8 * grp;
+    float ql4[4];  // G1L: the query's dims 4 (lane%16) .. +3, log2-score units
+    if constexpr (G1L) {
+        const float4 x = *reinterpret_cast<const float4*>(q + 4 * (lane & 15));
+        const float f = a.qscale * a.score_l2;
+        ql4[0] = x.x * f;
+        ql4[1] = x.y * f;
+        ql4[2] = x.z * f;
+        ql4[3] = x.w * f;
+    }
     float4 qx[NS][2];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = 0; s < NS && !G1L; ++s) {
         qx[s][0] = reinterpret_cast<const float4*>(qc + 32 * s)[0];
         qx[s][1] = reinterpret_cast<const float4*>(qc + 32 * s)[1];
     }
     half8 qh[NS], ql[NS];
     float qv[NS][8];  // G1: the query in f32, log2-score units
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = 0; s < NS && !G1L; ++s) {
         const float x[8] = {qx[s][0].x, qx[s][0].y, qx[s][0].z, qx[s][0].w,
                             qx[s][1].x, qx[s][1].y, qx[s][1].z, qx[s][1].w};
 #pragma unroll
@@ -942,6 +1077,9 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     float m_run = ninf(), l_run = 0.0f;
     floatx4 o[NT];
     float o1[NT];  // G1: lane's context sums for dims 16t + col
+    float ol[8];   // G1L: lane's context sums for dims 8i + lane/8
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ol[i] = 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         o[t] = zero_f4();
@@ -949,7 +1087,9 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     }
     auto fold = [&](const FR& f, int p, auto mask_tag) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        if constexpr (G1)
+        if constexpr (G1L)
+            fold_block_g1l<HD, MASK>(f, ql4, p, tk, lane, m_run, l_run, ol, prow[wave]);
+        else if constexpr (G1)
             fold_block_g1<HD, KIND, MASK>(f, qv, p, tk, col, grp, m_run, l_run, o1, prow[wave]);
         else
             fold_block<HD, KIND, MASK>(f, qh, ql, p, tk, grp, a.score_l2, m_run, l_run, o);
@@ -994,7 +1134,10 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         ld(nfull * 32, f0, std::integral_constant<bool, TILED>{});
         fold(f0, nfull * 32, std::true_type{});
     }
-    if constexpr (G1) {
+    float olc = 0.0f;
+    if constexpr (G1L) {
+        olc = g1l_context(ol, lane);
+    } else if constexpr (G1) {
         // A wave with no block keeps m = -inf, l = 0, o = 0 (weight 0 below).
 #pragma unroll
         for (int t = 0; t < NT; ++t) o1[t] = sum4grp(o1[t]);
@@ -1010,7 +1153,9 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         wl[wave][col] = l_run;
     }
     float* ob = lds + wave * OBW;
-    if constexpr (G1) {
+    if constexpr (G1L) {
+        ob[8 * (lane & 7) + (lane >> 3)] = olc;
+    } else if constexpr (G1) {
         if (grp == 0) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) ob[16 * t + col] = o1[t];
