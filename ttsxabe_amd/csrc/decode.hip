@@ -246,17 +246,23 @@ __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<
             if constexpr (FULL) {
                 v_row8<KIND, VA, NTL>(c, row, h, l);
             } else {
+                // Element loads at a clamped key, all unconditional (a load
+                // under a lane-varying branch makes the compiler wait for it
+                // at the branch's end: one memory round trip per element).
+                const size_t rb = row - kb;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    if (kb + j < c.tk) {
-                        if constexpr (KIND == KV_F16) {
-                            h[j] = __builtin_bit_cast(half_t, reinterpret_cast<const uint16_t*>(c.v)[row + j]);
-                        } else {
-                            half_t hh, ll;
-                            split_h(reinterpret_cast<const float*>(c.v)[row + j], hh, ll);
-                            h[j] = hh;
-                            l[j] = ll;
-                        }
+                    const bool ok = kb + j < c.tk;
+                    const size_t e = rb + min(kb + j, c.tk - 1);
+                    if constexpr (KIND == KV_F16) {
+                        const uint16_t x = reinterpret_cast<const uint16_t*>(c.v)[e];
+                        h[j] = ok ? __builtin_bit_cast(half_t, x) : (half_t)0.0f;
+                    } else {
+                        const float x = reinterpret_cast<const float*>(c.v)[e];
+                        half_t hh, ll;
+                        split_h(ok ? x : 0.0f, hh, ll);
+                        h[j] = hh;
+                        l[j] = ll;
                     }
                 }
             }
@@ -729,9 +735,13 @@ __device__ __forceinline__ void load_block_f32v(const Ctx& c, int p0, int lane, 
             f.v[t][0] = make_float4(a0.x, a0.y, a1.x, a1.y);
             f.v[t][1] = make_float4(a2.x, a2.y, a3.x, a3.y);
         } else {
+            // Clamped, unconditional element loads (see load_block).
             float x[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = k0 + j < c.tk ? r[j] : 0.0f;
+            for (int j = 0; j < 8; ++j) {
+                const float y = r[min(k0 + j, c.tk - 1) - k0];
+                x[j] = k0 + j < c.tk ? y : 0.0f;
+            }
             f.v[t][0] = make_float4(x[0], x[1], x[2], x[3]);
             f.v[t][1] = make_float4(x[4], x[5], x[6], x[7]);
         }
@@ -776,9 +786,13 @@ __device__ __forceinline__ void load_block_f32l(const Ctx& c, int p0, int lane, 
             const float2 a0 = reinterpret_cast<const float2*>(r)[0], a1 = reinterpret_cast<const float2*>(r)[1];
             f.v[i] = make_float4(a0.x, a0.y, a1.x, a1.y);
         } else {
+            // Clamped, unconditional element loads (see load_block).
             float x[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) x[j] = k0 + j < c.tk ? r[j] : 0.0f;
+            for (int j = 0; j < 4; ++j) {
+                const float y = r[min(k0 + j, c.tk - 1) - k0];
+                x[j] = k0 + j < c.tk ? y : 0.0f;
+            }
             f.v[i] = make_float4(x[0], x[1], x[2], x[3]);
         }
     }
