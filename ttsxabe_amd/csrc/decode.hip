@@ -183,10 +183,11 @@ __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<
     const int col = lane & 15, grp = lane >> 4;
     if constexpr (KIND == KV_T16) {
         const half8* b = reinterpret_cast<const half8*>(c.k + (long)(p0 >> 5) * c.bstride);
+        // In the order the fold consumes them (dim block s outer, key tile T inner).
 #pragma unroll
-        for (int T = 0; T < 2; ++T)
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
-            for (int s = 0; s < NS; ++s) f.k[T][s] = __builtin_nontemporal_load(&b[(T * NS + s) * 64 + lane]);
+            for (int T = 0; T < 2; ++T) f.k[T][s] = __builtin_nontemporal_load(&b[(T * NS + s) * 64 + lane]);
         const half8* vb = b + 4 * HD;  // the V area: 32*HD halves in
 #pragma unroll
         for (int t = 0; t < NT; ++t) f.v[t] = __builtin_nontemporal_load(&vb[t * 64 + lane]);
@@ -293,11 +294,16 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
     constexpr int NS = HD / 32;
     constexpr int NT = HD / 16;
     float sc[8];
+    // The two key tiles' chains interleaved (s outer, T inner): each tile's
+    // accumulation order is unchanged, and the matrix unit always has an
+    // independent product to start while the other tile's waits on its
+    // predecessor.
+    floatx4 accs[2] = {zero_f4(), zero_f4()};
 #pragma unroll
-    for (int T = 0; T < 2; ++T) {
-        floatx4 acc = zero_f4();
+    for (int s = 0; s < NS; ++s) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
+        for (int T = 0; T < 2; ++T) {
+            floatx4& acc = accs[T];
             if constexpr (KIND == KV_F16 || KIND == KV_T16) {
                 acc = mfma16(f.k[T][s], qh[s], acc);
                 acc = mfma16(f.k[T][s], ql[s], acc);
@@ -319,9 +325,11 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
                 for (int r = 0; r < 4; ++r) acc[r] += (float)h_at(f.ks[s], 4 * T + r) * b[r];
             }
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sc[4 * T + r] = acc[r];
     }
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[4 * T + r] = accs[T][r];
     const int kb = p0 + 8 * grp;
     float mx = ninf();
 #pragma unroll

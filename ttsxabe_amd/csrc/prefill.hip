@@ -626,8 +626,12 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
                         float x[8];
 #pragma unroll
                         for (int j = 0; j < 8; ++j) {
+                            // Loaded unconditionally at the clamped key, then
+                            // selected: a load under a lane-varying condition
+                            // is waited for at the branch's end.
                             const int key = min(k0 + j, ktot - 1);
-                            x[j] = k0 + j < ktot ? vf32[svb + (size_t)d * a.cap + key] : 0.0f;
+                            const float y = vf32[svb + (size_t)d * a.cap + key];
+                            x[j] = k0 + j < ktot ? y : 0.0f;
                         }
                         v0 = make_float4(x[0], x[1], x[2], x[3]);
                         v1 = make_float4(x[4], x[5], x[6], x[7]);
