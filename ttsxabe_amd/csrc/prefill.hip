@@ -34,6 +34,7 @@
 #include "common.h"
 #include "prefill.h"
 #include "kvlayout.h"
+#include "lineorder.h"
 
 // LDS fragment reads kept in flight ahead of the MFMAs that use them in the
 // tile loop's software pipeline, at most the pipeline's reads (measured on
@@ -412,80 +413,10 @@ __global__ __launch_bounds__(PT) void flash_prefill_kernel(PrefillArgs a) {
 // (their scores are masked); V chunks past ktot may hold anything, so in the
 // one tile that reaches past ktot they are zeroed in LDS before use.
 //
-// The reference layout (PF_F16) is not gathered in fragment order: a
-// fragment's 16 keys (or 16 V^T rows) sit in 16 different 128-byte lines,
-// half of each, and a compute unit's rate of line requests then sets the
-// time to a tile (C3 at 512 rows: 17.1 us against 13.5 for the same tile
-// copied from the tiled cache). Its tiles are loaded in line order instead,
-// every instruction reading whole lines (1 KB = 8 lines):
-//   K: instruction f holds tile keys f * KPI .. + KPI - 1 (KPI = 64 / CR keys
-//      of CR = HD / 8 chunks of 16 bytes), lane l chunk position l % CR of
-//      key f * KPI + l / CR;
-//   V: instruction f holds dims 8f .. 8f + 7, lane l position l % 8 of dim
-//      8f + l / 8 (a V^T row's 64 tile keys are one line).
-// Within a key (dim) the chunk at position p is chunk p ^ sw of the row
-// (sw: pfl_ksw, pfl_vsw), so that the fragment reads, which take one chunk
-// of 16 different keys (dims) per 16 lanes, hit 16 different 16-byte bank
-// groups. The fragment reads gather through pfl_kslot / pfl_vslot.
-template <int HD>
-__device__ __forceinline__ int pfl_ksw(int k) {
-    // hd 128 (a row is 16 chunks, 4 keys an instruction): the read's lanes
-    // differ in k & 3 and (k >> 3) & 3; hd 64 (8 chunks, 8 keys): the slot's
-    // bank group is 8 (k & 1) + position, so the swizzle takes (k >> 1) & 1
-    // and (k >> 3) & 3.
-    return HD == 128 ? ((k & 3) | (((k >> 3) & 3) << 2)) : (((k >> 1) & 1) | (((k >> 3) & 3) << 1));
-}
-__device__ __forceinline__ int pfl_vsw(int d) { return (d >> 1) & 7; }
-// 16-byte slot of chunk c (dims 8c .. 8c + 7) of tile key k in the K area.
-template <int HD>
-__device__ __forceinline__ int pfl_kslot(int k, int c) {
-    constexpr int CR = HD / 8, KPI = 64 / CR;
-    return (k / KPI) * 64 + (k % KPI) * CR + (c ^ pfl_ksw<HD>(k));
-}
-// 16-byte slot of chunk c (tile keys 8c .. 8c + 7) of dim d in the V area.
-__device__ __forceinline__ int pfl_vslot(int d, int c) { return (d >> 3) * 64 + (d & 7) * 8 + (c ^ pfl_vsw(d)); }
-// One line-order load instruction of a reference-layout tile at kv0:
-// fragment index f < KF is K, else V (see above).
-template <int HD, int KF>
-__device__ __forceinline__ void pfl_issue(const half_t* kc, __amdgpu_buffer_rsrc_t rv, int f, int lane, size_t kh,
-                                          size_t cap, int kv0, int ktot, half_t* l) {
-    constexpr int CR = HD / 8, KPI = 64 / CR;
-    if (f < KF) {
-        const int k = f * KPI + lane / CR;
-        const int c = (lane % CR) ^ pfl_ksw<HD>(k);
-        const int key = min(kv0 + k, ktot - 1);
-        __builtin_amdgcn_global_load_lds(kc + (kh * cap + key) * HD + 8 * c, l, 16, 0, 0);
-    } else {
-        const int d = 8 * (f - KF) + (lane >> 3);
-        const int c = (lane & 7) ^ pfl_vsw(d);
-        const uint32_t off = (uint32_t)(((kh * HD + d) * cap + kv0 + 8 * c) * 2);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, l, 16, off, 0, 0, 0);
-    }
-}
-// Zero the V entries of keys >= ktot in the tile at kv0 (line order when LO,
-// else fragment order), threads tid, tid + nt, ... over the V area.
-template <int HD, bool LO>
-__device__ __forceinline__ void pf_zero_tail(half8* vf, int kv0, int ktot, int tid, int nt) {
-    constexpr int NT = HD / 16, VF = 2 * NT;
-    for (int c = tid; c < VF * 64; c += nt) {
-        int k0;
-        if constexpr (LO) {
-            const int d = 8 * (c >> 6) + ((c & 63) >> 3);
-            k0 = kv0 + 8 * ((c & 7) ^ pfl_vsw(d));
-        } else {
-            const int hf = c / (NT * 64), ln = c % 64;
-            k0 = kv0 + 32 * hf + 8 * (ln >> 4);
-        }
-        if (k0 + 8 > ktot) {
-            half8 x = vf[c];
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (k0 + j >= ktot) x[j] = (half_t)0.0f;
-            vf[c] = x;
-        }
-    }
-}
-
+// The reference layout (PF_F16) is held in line order (lineorder.h): a
+// fragment gathered straight from it would touch 16 lines, half of each, and
+// a compute unit's rate of line requests would set the time to a tile (C3 at
+// 512 rows: 17.1 us against 13.5 for the same tile from the tiled cache).
 // W: waves per workgroup, 4, or 8 for the encoder rows (NQT = 1: the tile
 // staging per query row of two query tiles per wave, at two waves per SIMD).
 // Where the staged stacked-rows V tile keeps MFMA operand lane `ln` of dim
