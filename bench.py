@@ -428,6 +428,10 @@ def main():
             "c3_prefill_128": lambda: bench_prefill(torch, g, 128, 32, 8, 128, a.steps, a.warmup, a.layers),
             "c3_prefill_8192_steady": lambda: bench_prefill(torch, g, 8192, 32, 8, 128, 5, 2, 4),
             "c3_prefill_512": lambda: bench_prefill(torch, g, 512, 32, 8, 128, a.steps, a.warmup, a.layers),
+            "c3_prefill_512_reference_layout": lambda: bench_prefill(torch, g, 512, 32, 8, 128, a.steps, a.warmup,
+                                                                     a.layers, tiled=False),
+            "c4_cross_decode_reference_layout": lambda: bench_decode_f16(torch, g, 20, 20, 64, 1500, 1500, True,
+                                                                         a.steps, a.warmup, a.layers),
             "c4_encoder": lambda: bench_encoder(torch, g, 1500, 20, 64, a.steps, a.warmup, a.layers),
             "c5_q8_batch_decode": lambda: bench_q8_batch(torch, g, a.steps, a.warmup),
             "practical_peaks": lambda: practical_peaks(torch),
