@@ -48,6 +48,14 @@ CASES = [
     # 4: V rows only 8-byte aligned; full blocks and a 14-key partial one.
     (5, 5, 64, 302, 450, False, False),
     (3, 3, 64, 450, 450, False, True),
+    # The last block running past the capacity (capacity not a multiple of
+    # 32), so its reads are clamped inside the cache: f16 with 16-byte rows,
+    # f32 group 1 at head_dim 64 (16-byte rows) and 128, f32 group 4 with
+    # 8-byte rows.
+    (8, 2, 128, 1000, 1000, True, False),
+    (4, 4, 64, 451, 452, False, True),
+    (2, 2, 128, 330, 332, False, False),
+    (8, 2, 128, 1001, 1002, False, False),
 ]
 
 

@@ -112,18 +112,23 @@ struct Ctx {
     int tk, cap;
 };
 
-// Eight consecutive V^T elements (one value row, keys kb..kb+7) off the
-// reference layout as f16 hi/lo or exact f16. VA is the alignment the row
-// start guarantees (16 or 8 bytes).
+// Keys key0 .. key0 + 7 of one V^T row (rb: the row's first element) of the
+// reference layout, as f16 hi/lo or exact f16. VA is the alignment the row
+// start guarantees (16 or 8 bytes), which makes the row a whole number of
+// granules (VA bytes); a granule that would pass the cache's capacity is read
+// from the row's start instead (its keys are past tk, and the fold zeroes
+// them), so no block reads outside the row, whatever tk.
 template <int KIND, int VA, bool NTL = false>
-__device__ __forceinline__ void v_row8(const Ctx& c, size_t row, half8& h, half8& l) {
+__device__ __forceinline__ void v_row8(const Ctx& c, size_t rb, int key0, half8& h, half8& l) {
+    constexpr int ESZ = KIND == KV_F16 ? 2 : 4, G = VA / ESZ;  // elements per granule
+    auto at = [&](int g) { return rb + (key0 + G * (g + 1) <= c.cap ? key0 + G * g : 0); };
     if constexpr (KIND == KV_F16) {
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(c.v) + row;
+        const uint16_t* v = reinterpret_cast<const uint16_t*>(c.v);
         if constexpr (VA == 16) {
-            h = NTL ? __builtin_nontemporal_load(reinterpret_cast<const half8*>(p)) : ld_h8(p);
+            h = NTL ? __builtin_nontemporal_load(reinterpret_cast<const half8*>(v + at(0))) : ld_h8(v + at(0));
         } else {
-            const uint2 a = reinterpret_cast<const uint2*>(p)[0];
-            const uint2 b = reinterpret_cast<const uint2*>(p)[1];
+            const uint2 a = *reinterpret_cast<const uint2*>(v + at(0));
+            const uint2 b = *reinterpret_cast<const uint2*>(v + at(1));
             const uint32_t w[4] = {a.x, a.y, b.x, b.y};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -132,19 +137,19 @@ __device__ __forceinline__ void v_row8(const Ctx& c, size_t row, half8& h, half8
             }
         }
     } else {
-        const float* p = reinterpret_cast<const float*>(c.v) + row;
+        const float* v = reinterpret_cast<const float*>(c.v);
         float x[8];
         if constexpr (VA == 16) {
-            const float4 a = reinterpret_cast<const float4*>(p)[0];
-            const float4 b = reinterpret_cast<const float4*>(p)[1];
+            const float4 a = *reinterpret_cast<const float4*>(v + at(0));
+            const float4 b = *reinterpret_cast<const float4*>(v + at(1));
             x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
             x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                const float2 a = reinterpret_cast<const float2*>(p + j)[0];
-                x[j] = a.x;
-                x[j + 1] = a.y;
+            for (int g = 0; g < 4; ++g) {
+                const float2 a = *reinterpret_cast<const float2*>(v + at(g));
+                x[2 * g] = a.x;
+                x[2 * g + 1] = a.y;
             }
         }
 #pragma unroll
@@ -173,10 +178,12 @@ __device__ __forceinline__ uint4 ld_stream16(const uint4* p) {
 // layout 10.16 -> 9.94 us) but not on the group-1 path, whose loads share
 // lines in a pattern the evict-first policy hurts (the MHA decode at 4000
 // positions went 22.1 -> 23.9 us).
-// Reference layouts: FULL = every key of the block is live, so nothing is
-// guarded; !FULL = the one partial block at the end of the context, where
-// keys >= tk read as zero and nothing past tk is touched.
-template <int HD, int KIND, int VA, bool FULL, bool NTL = false>
+// Reference layouts: every block is read the same way, the context's partial
+// last block included: K rows past the capacity are clamped to its last row,
+// V granules past it to the row's start (v_row8), so nothing outside the
+// cache is read, and whatever lies past tk is left to the fold's mask (scores
+// to -inf, values to zero).
+template <int HD, int KIND, int VA, bool NTL = false>
 __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<HD, KIND>& f) {
     constexpr int NS = HD / 32;
     constexpr int NT = HD / 16;
@@ -212,16 +219,13 @@ __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<
     } else {
 #pragma unroll
         for (int T = 0; T < 2; ++T) {
-            const int key = p0 + 8 * (col >> 2) + 4 * T + (col & 3);
-            const bool ok = FULL || key < c.tk;
-            const int kk = ok ? key : 0;
+            const int kk = min(p0 + 8 * (col >> 2) + 4 * T + (col & 3), c.cap - 1);
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
                 const int d0 = 32 * s + 8 * grp;
                 if constexpr (KIND == KV_F16) {
                     const half8* kp = reinterpret_cast<const half8*>(c.k + ((size_t)kk * HD + d0) * 2);
-                    const half8 x = NTL ? __builtin_nontemporal_load(kp) : *kp;
-                    f.k[T][s] = ok ? x : zero_h8();
+                    f.k[T][s] = NTL ? __builtin_nontemporal_load(kp) : *kp;
                 } else {
                     const float4* p = reinterpret_cast<const float4*>(c.k + ((size_t)kk * HD + d0) * 4);
                     const float4 a = p[0], b = p[1];
@@ -230,7 +234,7 @@ __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         half_t hh, ll;
-                        split_h(ok ? x[j] : 0.0f, hh, ll);
+                        split_h(x[j], hh, ll);
                         h[j] = hh;
                         l[j] = ll;
                     }
@@ -242,31 +246,8 @@ __device__ __forceinline__ void load_block(const Ctx& c, int p0, int lane, Frag<
         const int kb = p0 + 8 * grp;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const size_t row = (size_t)(16 * t + col) * c.cap + kb;
             half8 h = zero_h8(), l = zero_h8();
-            if constexpr (FULL) {
-                v_row8<KIND, VA, NTL>(c, row, h, l);
-            } else {
-                // Element loads at a clamped key, all unconditional (a load
-                // under a lane-varying branch makes the compiler wait for it
-                // at the branch's end: one memory round trip per element).
-                const size_t rb = row - kb;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const bool ok = kb + j < c.tk;
-                    const size_t e = rb + min(kb + j, c.tk - 1);
-                    if constexpr (KIND == KV_F16) {
-                        const uint16_t x = reinterpret_cast<const uint16_t*>(c.v)[e];
-                        h[j] = ok ? __builtin_bit_cast(half_t, x) : (half_t)0.0f;
-                    } else {
-                        const float x = reinterpret_cast<const float*>(c.v)[e];
-                        half_t hh, ll;
-                        split_h(ok ? x : 0.0f, hh, ll);
-                        h[j] = hh;
-                        l[j] = ll;
-                    }
-                }
-            }
+            v_row8<KIND, VA, NTL>(c, (size_t)(16 * t + col) * c.cap, kb, h, l);
             if constexpr (KIND == KV_F32) {
                 f.vh[t] = h;
                 f.vl[t] = l;
@@ -406,12 +387,11 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            if constexpr (KIND == KV_F16) {
-                o[t] = mfma16(f.v[t], ph, o[t]);
-                o[t] = mfma16(f.v[t], pl, o[t]);
-            } else if constexpr (KIND == KV_T16) {
-                // A tiled cache holds garbage past tk: zero those keys' values so
-                // that 0 * (a non-finite half) cannot reach the sum.
+            if constexpr (KIND == KV_F16 || KIND == KV_T16) {
+                // A cache may hold anything past tk (the tiled cache's block
+                // tail, the reference layout's unused capacity, clamped reads):
+                // zero those keys' values so that 0 * (a non-finite half)
+                // cannot reach the sum.
                 half8 vv = f.v[t];
                 if constexpr (MASK) {
 #pragma unroll
@@ -420,9 +400,17 @@ __device__ __forceinline__ void fold_block(const Frag<HD, KIND>& f, const half8 
                 o[t] = mfma16(vv, ph, o[t]);
                 o[t] = mfma16(vv, pl, o[t]);
             } else {
-                o[t] = mfma16(f.vh[t], ph, o[t]);
-                o[t] = mfma16(f.vh[t], pl, o[t]);
-                o[t] = mfma16(f.vl[t], ph, o[t]);
+                half8 vh = f.vh[t], vl = f.vl[t];
+                if constexpr (MASK) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        vh[j] = (kb + j < tk) ? vh[j] : (half_t)0.0f;
+                        vl[j] = (kb + j < tk) ? vl[j] : (half_t)0.0f;
+                    }
+                }
+                o[t] = mfma16(vh, ph, o[t]);
+                o[t] = mfma16(vh, pl, o[t]);
+                o[t] = mfma16(vl, ph, o[t]);
             }
         }
     }
@@ -708,9 +696,9 @@ struct FragF32 {
     float4 v[HD / 16][2];
 };
 
-// The 32-key block at p0 of an f32 reference-layout cache, raw. FULL: every
-// key of the block is live; else keys >= tk read as zero.
-template <int HD, int VA, bool FULL>
+// The 32-key block at p0 of an f32 reference-layout cache, raw, read as
+// load_block reads it (rows and granules clamped inside the capacity).
+template <int HD, int VA>
 __device__ __forceinline__ void load_block_f32v(const Ctx& c, int p0, int lane, FragF32<HD>& f) {
     constexpr int NS = HD / 32, NT = HD / 16;
     const int col = lane & 15, grp = lane >> 4;
@@ -718,40 +706,27 @@ __device__ __forceinline__ void load_block_f32v(const Ctx& c, int p0, int lane, 
     const float* vb = reinterpret_cast<const float*>(c.v);
 #pragma unroll
     for (int T = 0; T < 2; ++T) {
-        const int key = p0 + 8 * (col >> 2) + 4 * T + (col & 3);
-        const bool ok = FULL || key < c.tk;
-        const int kk = ok ? key : 0;
+        const int kk = min(p0 + 8 * (col >> 2) + 4 * T + (col & 3), c.cap - 1);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const float4* p = reinterpret_cast<const float4*>(kb + (size_t)kk * HD + 32 * s + 8 * grp);
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 x0 = p[0], x1 = p[1];
-            f.k[T][s][0] = ok ? x0 : z;
-            f.k[T][s][1] = ok ? x1 : z;
+            f.k[T][s][0] = p[0];
+            f.k[T][s][1] = p[1];
         }
     }
     const int k0 = p0 + 8 * grp;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const float* r = vb + (size_t)(16 * t + col) * c.cap + k0;
-        if constexpr (FULL && VA == 16) {
-            f.v[t][0] = reinterpret_cast<const float4*>(r)[0];
-            f.v[t][1] = reinterpret_cast<const float4*>(r)[1];
-        } else if constexpr (FULL) {
-            const float2 a0 = reinterpret_cast<const float2*>(r)[0], a1 = reinterpret_cast<const float2*>(r)[1];
-            const float2 a2 = reinterpret_cast<const float2*>(r)[2], a3 = reinterpret_cast<const float2*>(r)[3];
+        const size_t rb = (size_t)(16 * t + col) * c.cap;
+        auto at = [&](int g, int G) { return vb + rb + (k0 + G * (g + 1) <= c.cap ? k0 + G * g : 0); };
+        if constexpr (VA == 16) {
+            f.v[t][0] = *reinterpret_cast<const float4*>(at(0, 4));
+            f.v[t][1] = *reinterpret_cast<const float4*>(at(1, 4));
+        } else {
+            const float2 a0 = *reinterpret_cast<const float2*>(at(0, 2)), a1 = *reinterpret_cast<const float2*>(at(1, 2));
+            const float2 a2 = *reinterpret_cast<const float2*>(at(2, 2)), a3 = *reinterpret_cast<const float2*>(at(3, 2));
             f.v[t][0] = make_float4(a0.x, a0.y, a1.x, a1.y);
             f.v[t][1] = make_float4(a2.x, a2.y, a3.x, a3.y);
-        } else {
-            // Clamped, unconditional element loads (see load_block).
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float y = r[min(k0 + j, c.tk - 1) - k0];
-                x[j] = k0 + j < c.tk ? y : 0.0f;
-            }
-            f.v[t][0] = make_float4(x[0], x[1], x[2], x[3]);
-            f.v[t][1] = make_float4(x[4], x[5], x[6], x[7]);
         }
     }
 }
@@ -772,36 +747,26 @@ struct FragF32L {
     float4 v[8];
 };
 
-template <int HD, int VA, bool FULL>
+template <int HD, int VA>
 __device__ __forceinline__ void load_block_f32l(const Ctx& c, int p0, int lane, FragF32L<HD>& f) {
     const float* kb = reinterpret_cast<const float*>(c.k);
     const float* vb = reinterpret_cast<const float*>(c.v);
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int key = p0 + 4 * i + (lane >> 4);
-        const bool ok = FULL || key < c.tk;
-        const float4 x = *reinterpret_cast<const float4*>(kb + (size_t)(ok ? key : 0) * HD + 4 * (lane & 15));
-        f.k[i] = ok ? x : z;
+        const int key = min(p0 + 4 * i + (lane >> 4), c.cap - 1);
+        f.k[i] = *reinterpret_cast<const float4*>(kb + (size_t)key * HD + 4 * (lane & 15));
     }
     const int k0 = p0 + 4 * (lane & 7);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float* r = vb + (size_t)(8 * i + (lane >> 3)) * c.cap + k0;
-        if constexpr (FULL && VA == 16) {
-            f.v[i] = *reinterpret_cast<const float4*>(r);
-        } else if constexpr (FULL) {
-            const float2 a0 = reinterpret_cast<const float2*>(r)[0], a1 = reinterpret_cast<const float2*>(r)[1];
-            f.v[i] = make_float4(a0.x, a0.y, a1.x, a1.y);
+        // Granules past the capacity read from the row's start (see v_row8).
+        const float* rb = vb + (size_t)(8 * i + (lane >> 3)) * c.cap;
+        if constexpr (VA == 16) {
+            f.v[i] = *reinterpret_cast<const float4*>(rb + (k0 + 4 <= c.cap ? k0 : 0));
         } else {
-            // Clamped, unconditional element loads (see load_block).
-            float x[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float y = r[min(k0 + j, c.tk - 1) - k0];
-                x[j] = k0 + j < c.tk ? y : 0.0f;
-            }
-            f.v[i] = make_float4(x[0], x[1], x[2], x[3]);
+            const float2 a0 = *reinterpret_cast<const float2*>(rb + (k0 + 2 <= c.cap ? k0 : 0));
+            const float2 a1 = *reinterpret_cast<const float2*>(rb + (k0 + 4 <= c.cap ? k0 + 2 : 0));
+            f.v[i] = make_float4(a0.x, a0.y, a1.x, a1.y);
         }
     }
 }
@@ -861,12 +826,21 @@ __device__ __forceinline__ void fold_block_g1l(const FragF32L<HD>& f, const floa
     if (!(lane & 1)) pw[kl] = e;
     __builtin_amdgcn_wave_barrier();
     const float4 pp = *reinterpret_cast<const float4*>(pw + 4 * (lane & 7));
+    const int k0 = p0 + 4 * (lane & 7);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        float acc = __builtin_fmaf(pp.x, f.v[i].x, o[i]);
-        acc = __builtin_fmaf(pp.y, f.v[i].y, acc);
-        acc = __builtin_fmaf(pp.z, f.v[i].z, acc);
-        o[i] = __builtin_fmaf(pp.w, f.v[i].w, acc);
+        float4 v = f.v[i];
+        if constexpr (MASK) {
+            // Values past tk may be anything (unused capacity, clamped reads).
+            v.x = k0 < tk ? v.x : 0.0f;
+            v.y = k0 + 1 < tk ? v.y : 0.0f;
+            v.z = k0 + 2 < tk ? v.z : 0.0f;
+            v.w = k0 + 3 < tk ? v.w : 0.0f;
+        }
+        float acc = __builtin_fmaf(pp.x, v.x, o[i]);
+        acc = __builtin_fmaf(pp.y, v.y, acc);
+        acc = __builtin_fmaf(pp.z, v.z, acc);
+        o[i] = __builtin_fmaf(pp.w, v.w, acc);
     }
     __builtin_amdgcn_wave_barrier();  // the row is read before the next block's writes
 }
@@ -952,8 +926,8 @@ __device__ __forceinline__ void fold_block_g1(const FR& f, const float (&qv)[HD 
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             float v = g1_v<HD, KIND>(f, t, j);
-            // A tiled cache may hold non-finite garbage past tk: 0 * NaN is NaN.
-            if constexpr (MASK && KIND == KV_T16) v = p0 + 8 * grp + j < tk ? v : 0.0f;
+            // A cache may hold non-finite garbage past tk: 0 * NaN is NaN.
+            if constexpr (MASK) v = p0 + 8 * grp + j < tk ? v : 0.0f;
             acc = __builtin_fmaf(pp[j], v, acc);
         }
         o[t] = acc;
@@ -1034,26 +1008,33 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
         c.v = reinterpret_cast<const char*>(a.v) + kvh * HD * a.cap * esz;
     }
 
-    // This wave's blocks: b_i = first + i * DW for i < nit; full blocks first,
-    // through a two-deep pipeline (block i+1's loads in flight while block i
-    // is folded), then the context's one partial block if it is this wave's.
-    // The first block's loads go out before the queries are read.
+    // This wave's blocks: b_i = first + i * DW for i < nb, through a two-deep
+    // pipeline (block i+1's loads in flight while block i is folded). The
+    // context's partial last block, when it is this wave's, is its last (nf
+    // full blocks, then it): every block is loaded the same way, and only the
+    // partial one is folded with the mask. The first blocks' loads go out
+    // before the queries are read.
     const int first = split * DW * nit + wave;
     const int nfull = tk >> 5;
     const int nf = nfull > first ? min(nit, (nfull - first + DW - 1) / DW) : 0;
     const bool tail = (tk & 31) && nfull >= first && (nfull - first) % DW == 0 && (nfull - first) / DW < nit;
+    // Tiled caches keep the partial block out of the pipeline (loaded and
+    // folded after it): with it inside, the pipeline's epilogue needs both
+    // fold variants for both register sets, which cost the tiled decode
+    // ~0.05 us (C2 9.39 -> 9.44 us) for a gain only partial blocks see.
+    constexpr bool TP = !TILED;  // the partial block inside the pipeline
+    const int nb = nf + (TP && tail ? 1 : 0);
     FR f0, f1;
-    auto ld = [&](int p, FR& f, auto full_tag) __attribute__((always_inline)) {
-        constexpr bool FULL = decltype(full_tag)::value;
-        if constexpr (G1L) load_block_f32l<HD, VA, FULL>(c, p, lane, f);
-        else if constexpr (G1 && KIND == KV_F32) load_block_f32v<HD, VA, FULL>(c, p, lane, f);
-        else load_block<HD, KIND, VA, FULL, !G1>(c, p, lane, f);
+    auto ld = [&](int p, FR& f) __attribute__((always_inline)) {
+        if constexpr (G1L) load_block_f32l<HD, VA>(c, p, lane, f);
+        else if constexpr (G1 && KIND == KV_F32) load_block_f32v<HD, VA>(c, p, lane, f);
+        else load_block<HD, KIND, VA, !G1>(c, p, lane, f);
     };
     // The first two blocks go out before the queries are read: the queries'
     // first use waits for every load issued before them, so a block issued
     // after that would start a second memory round trip.
-    if (nf > 0) ld(first * 32, f0, std::true_type{});
-    if (nf > 1 && !(KIND == KV_F32 && HD == 128)) ld((first + DW) * 32, f1, std::true_type{});
+    if (nb > 0) ld(first * 32, f0);
+    if (nb > 1 && !(KIND == KV_F32 && HD == 128)) ld((first + DW) * 32, f1);
 
     // The group's queries as B operands, hi + lo (columns past the group are
     // read from column 0 and zeroed, so every load is unconditional). The
@@ -1128,32 +1109,39 @@ __global__ __launch_bounds__(DT, KIND == KV_F32 ? 1 : 2) void attn_decode_kernel
     // f32 caches at head_dim 128: one block in flight (two would not fit in
     // the register file and would spill to scratch).
     constexpr bool DEEP = !(KIND == KV_F32 && HD == 128);
+    // Block j of the wave, folded with the mask when it is the partial one.
+    auto fold_j = [&](const FR& f, int j) __attribute__((always_inline)) {
+        const int p = (first + j * DW) * 32;
+        if (TP && tail && j == nf) fold(f, p, std::true_type{});
+        else fold(f, p, std::false_type{});
+    };
     int i = 0;
     if constexpr (!DEEP) {
-        for (; i < nf; ++i) {
-            if (i > 0) ld((first + i * DW) * 32, f0, std::true_type{});
-            fold(f0, (first + i * DW) * 32, std::false_type{});
+        for (; i < nb; ++i) {
+            if (i > 0) ld((first + i * DW) * 32, f0);
+            fold_j(f0, i);
         }
     }
-    for (; DEEP && i + 2 < nf; i += 2) {
+    // Blocks i, i + 1 are full here (only the last block can be partial).
+    for (; DEEP && i + 2 < nb; i += 2) {
         const int p0 = (first + i * DW) * 32;
         const int p1 = (first + (i + 1) * DW) * 32;
         const int p2 = (first + (i + 2) * DW) * 32;
-        const int p3 = (first + min(i + 3, nf - 1) * DW) * 32;
+        const int p3 = (first + min(i + 3, nb - 1) * DW) * 32;
         fold(f0, p0, std::false_type{});
         __builtin_amdgcn_sched_barrier(0);
-        ld(p2, f0, std::true_type{});
+        ld(p2, f0);
         __builtin_amdgcn_sched_barrier(0);
         fold(f1, p1, std::false_type{});
         __builtin_amdgcn_sched_barrier(0);
-        ld(p3, f1, std::true_type{});
+        ld(p3, f1);
         __builtin_amdgcn_sched_barrier(0);
     }
     // The last one or two blocks (already in f0, f1).
-    if (DEEP && i < nf) fold(f0, (first + i * DW) * 32, std::false_type{});
-    if (DEEP && i + 1 < nf) fold(f1, (first + (i + 1) * DW) * 32, std::false_type{});
-    if (tail) {
-        ld(nfull * 32, f0, std::integral_constant<bool, TILED>{});
+    if (DEEP && i < nb) fold_j(f0, i);
+    if (DEEP && i + 1 < nb) fold_j(f1, i + 1);
+    if (!TP && tail) {
+        ld(nfull * 32, f0);
         fold(f0, nfull * 32, std::true_type{});
     }
     float olc = 0.0f;
