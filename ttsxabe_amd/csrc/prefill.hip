@@ -505,7 +505,7 @@ __device__ __forceinline__ void softmax_tile(floatx4 (&sc)[2][2][NQT], int u, in
     l += ps;
 }
 
-template <int HD, int KIND, int NQT, int W>
+template <int HD, int KIND, int NQT, int W, bool QL>
 __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(PrefillArgs a) {
     static_assert(W == PW || (W == 8 && KIND == PF_ROWS), "eight waves: encoder rows only");
     constexpr int TW = W * LLMTIE_WAVE;
@@ -727,28 +727,68 @@ __global__ __launch_bounds__(W * LLMTIE_WAVE, 8 / W) void flash_fwd_kernel(Prefi
         if (kend > 0) issue(0, t0);
     }
     const float qsc = a.scale_q ? a.scale : 1.0f;
-    float4 qx[NQT][NS][2];
-#pragma unroll
-    for (int u = 0; u < NQT; ++u) {
-        const int r = min(p0 + 16 * u + col, a.tq - 1);
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const float4* p = reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 32 * s + 8 * grp);
-            qx[u][s][0] = p[0];
-            qx[u][s][1] = p[1];
-        }
-    }
     half8 qb[NQT][NS];
+    if constexpr (QL) {
+        // QL: the wave's query rows read in line order (each instruction 1
+        // KB of whole rows: RPI rows of LPR lanes x 4 floats), scaled,
+        // rounded to f16 and passed through this wave's part of buffer t1
+        // (free until the second tile is issued, after the first barrier)
+        // into fragment order. Read straight in fragment order, each
+        // instruction touches 16 rows' lines, half of each, which a launch
+        // of few workgroups (one per compute unit, or fewer) pays in its
+        // time to first tile. In t1 a row's 16-byte chunk c sits at
+        // position c ^ qsw(row), so a fragment read's 16 rows hit 16
+        // different bank groups.
+        constexpr int LPR = HD / 4, RPI = 64 / LPR, NI = QPW / RPI;
+        static_assert(W * QPW * HD <= (KF + VF) * FH, "the queries fit buffer t1");
+        auto qsw = [](int row) { return HD == 128 ? (row & 15) : ((row >> 1) & 7); };
+        half_t* qs = t1 + wave * QPW * HD;
+        float4 qx[NI];
 #pragma unroll
-    for (int u = 0; u < NQT; ++u) {
-        const float m = p0 + 16 * u + col < a.tq ? qsc : 0.0f;
+        for (int i = 0; i < NI; ++i) {
+            const int r = min(p0 + i * RPI + lane / LPR, a.tq - 1);
+            qx[i] = *reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 4 * (lane % LPR));
+        }
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const float4 x0 = qx[u][s][0], x1 = qx[u][s][1];
-            half8 x;
-            x[0] = to_h(x0.x * m); x[1] = to_h(x0.y * m); x[2] = to_h(x0.z * m); x[3] = to_h(x0.w * m);
-            x[4] = to_h(x1.x * m); x[5] = to_h(x1.y * m); x[6] = to_h(x1.z * m); x[7] = to_h(x1.w * m);
-            qb[u][s] = x;
+        for (int i = 0; i < NI; ++i) {
+            const int row = i * RPI + lane / LPR;
+            const float m = p0 + row < a.tq ? qsc : 0.0f;
+            half4 y;
+            y[0] = to_h(qx[i].x * m); y[1] = to_h(qx[i].y * m); y[2] = to_h(qx[i].z * m); y[3] = to_h(qx[i].w * m);
+            const int c = (lane % LPR) >> 1;
+            *reinterpret_cast<half4*>(qs + row * HD + (c ^ qsw(row)) * 8 + (lane & 1) * 4) = y;
+        }
+#pragma unroll
+        for (int u = 0; u < NQT; ++u)
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int row = 16 * u + col;
+                qb[u][s] = *reinterpret_cast<const half8*>(qs + row * HD + ((4 * s + grp) ^ qsw(row)) * 8);
+            }
+    } else {
+        float4 qx[NQT][NS][2];
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) {
+            const int r = min(p0 + 16 * u + col, a.tq - 1);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const float4* p =
+                    reinterpret_cast<const float4*>(a.q + (size_t)r * a.qs + (size_t)h * HD + 32 * s + 8 * grp);
+                qx[u][s][0] = p[0];
+                qx[u][s][1] = p[1];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NQT; ++u) {
+            const float m = p0 + 16 * u + col < a.tq ? qsc : 0.0f;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const float4 x0 = qx[u][s][0], x1 = qx[u][s][1];
+                half8 x;
+                x[0] = to_h(x0.x * m); x[1] = to_h(x0.y * m); x[2] = to_h(x0.z * m); x[3] = to_h(x0.w * m);
+                x[4] = to_h(x1.x * m); x[5] = to_h(x1.y * m); x[6] = to_h(x1.z * m); x[7] = to_h(x1.w * m);
+                qb[u][s] = x;
+            }
         }
     }
 
@@ -1215,19 +1255,31 @@ hipError_t launch_prefill(int hd, int kind, int nqt, const PrefillArgs& a, hipSt
         const int heavy = (a.past + a.tq + KT - 1) / KT;
         b.light_tiles = a.causal && !w8 && (int)items <= a.cus && heavy >= 6 && LLMTIE_PF_SLEEP > 0 ? heavy / 2 : 0;
         const dim3 g = b.xcd ? dim3(items) : grid;
+        // Line-order query loads (QL) where they pay: f16-cache launches of
+        // at most half a workgroup per compute unit (C3 at 128 rows 6.52 ->
+        // 6.30 us). At one workgroup per compute unit (C3 at 512 rows) they
+        // cost 0.2 us, and the encoder rows measured within noise.
+        const bool ql = (int)items * 2 <= a.cus && !getenv("LLMTIE_PREFILL_NOQL");
         if (w8) {
-            hipLaunchKernelGGL((flash_fwd_kernel<64, PF_ROWS, 1, 8>), g, block, 0, st, b);
+            hipLaunchKernelGGL((flash_fwd_kernel<64, PF_ROWS, 1, 8, false>), g, block, 0, st, b);
             return hipGetLastError();
         }
 #define F(HD, KIND, NQ)                                                                    \
     if (hd == HD && kind == KIND && nqt == NQ) {                                           \
-        hipLaunchKernelGGL((flash_fwd_kernel<HD, KIND, NQ, PW>), g, block, 0, st, b);      \
+        hipLaunchKernelGGL((flash_fwd_kernel<HD, KIND, NQ, PW, false>), g, block, 0, st, b); \
         return hipGetLastError();                                                          \
     }
+#define FQ(HD, KIND, NQ)                                                                   \
+    if (hd == HD && kind == KIND && nqt == NQ && ql) {                                     \
+        hipLaunchKernelGGL((flash_fwd_kernel<HD, KIND, NQ, PW, true>), g, block, 0, st, b); \
+        return hipGetLastError();                                                          \
+    }
+        FQ(64, PF_F16, 1) FQ(128, PF_F16, 1) FQ(64, PF_T16, 1) FQ(128, PF_T16, 1)
         F(64, PF_F16, 1) F(64, PF_F16, 2) F(128, PF_F16, 1) F(128, PF_F16, 2)
         F(64, PF_T16, 1) F(64, PF_T16, 2) F(128, PF_T16, 1) F(128, PF_T16, 2)
         F(64, PF_F32, 1) F(64, PF_F32, 2) F(128, PF_F32, 1) F(128, PF_F32, 2)
         F(64, PF_ROWS, 1) F(64, PF_ROWS, 2)
+#undef FQ
 #undef F
     }
     LK(64, PF_F16) LK(128, PF_F16) LK(64, PF_F32) LK(128, PF_F32) LK(64, PF_ROWS) LK(64, PF_T16) LK(128, PF_T16)
