@@ -56,6 +56,12 @@ CASES = [
     (4, 4, 64, 451, 452, False, True),
     (2, 2, 128, 330, 332, False, False),
     (8, 2, 128, 1001, 1002, False, False),
+    # One live key, and a partial block of one key after a full one, on the
+    # group-1 folds (f32 line order, f16, f32 at head_dim 128).
+    (4, 4, 64, 1, 452, False, True),
+    (4, 4, 64, 33, 452, False, True),
+    (4, 4, 64, 33, 452, True, True),
+    (2, 2, 128, 1, 64, False, False),
 ]
 
 
