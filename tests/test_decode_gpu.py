@@ -103,6 +103,35 @@ def test_the_fused_decode_attention_matches_the_chain(gpu, i):
     assert err < 2e-5 + own, f"case {CASES[i]}: {err:.3e} of full scale from the chain (its own error {own:.2e})"
 
 
+# Contexts whose last block is partial, one per loader: f16 group 4 and 1,
+# f32 group 1 at head_dim 64 (line order) and 128, f32 group 4, and blocks
+# running past the capacity.
+GARBAGE_CASES = [(8, 2, 128, 65, 256, True, False), (6, 6, 64, 1499, 1500, True, True),
+                 (6, 6, 64, 37, 448, False, True), (4, 4, 64, 33, 452, False, True),
+                 (2, 2, 128, 330, 332, False, False), (8, 2, 128, 1001, 1002, False, False),
+                 (4, 4, 64, 33, 452, True, True)]
+
+
+@pytest.mark.parametrize("case", GARBAGE_CASES)
+def test_positions_past_tk_never_reach_the_context(gpu, case):
+    """The reference layouts' last block may read positions tk .. cap - 1:
+    filled with NaN there, the context is bit-identical to the finite fill."""
+    from ttsxabe_amd.gpu import DecodeScratch
+    heads, kv, hd, tk, cap, half, scale_q = case
+    q = oracle.seq(heads * hd, 7)
+    k0 = oracle.seq(kv * cap * hd, 8).reshape(kv, cap, hd)
+    v0 = oracle.seq(kv * hd * cap, 9).reshape(kv, hd, cap)
+    kn, vn = k0.copy(), v0.copy()
+    kn[:, tk:, :] = np.nan
+    vn[:, :, tk:] = np.nan
+    put = up_f16 if half else up
+    f = gpu.attn_decode_f16 if half else gpu.attn_decode
+    s = DecodeScratch()
+    a = down(f(up(q), put(k0.ravel()), put(v0.ravel()), heads, kv, hd, tk, cap, 0.11, scale_q, s))
+    b = down(f(up(q), put(kn.ravel()), put(vn.ravel()), heads, kv, hd, tk, cap, 0.11, scale_q, s))
+    assert np.isfinite(b).all() and np.array_equal(a, b)
+
+
 def test_decode_refusals(gpu):
     from ttsxabe_amd.gpu import DecodeScratch, UnsupportedAttention, CacheOverrun
     s = DecodeScratch()
