@@ -52,6 +52,28 @@ def fused_attention_sized(gpu, heads, kv, hd, causal, tq, past, cap, half):
     assert worst < 0.5, f"worst error is {worst} of its tolerance"
 
 
+@pytest.mark.parametrize("args", [(4, 2, 128, True, 70, 33, 160, True), (4, 4, 64, False, 100, 0, 130, True),
+                                  (8, 2, 128, True, 300, 20, 400, True), (4, 2, 128, False, 70, 33, 160, False),
+                                  (4, 4, 64, True, 100, 7, 130, False)])
+def test_cache_positions_past_the_keys_never_reach_the_context(gpu, args):
+    """A reference-layout tile reaching past ktot = past + tq reads positions
+    up to the capacity; filled with NaN there, the result is bit-identical."""
+    heads, kv, hd, causal, tq, past, cap, half = args
+    tk = past + tq
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    q = up(oracle.seq(tq * heads * hd, 71))
+    kc, vc = caches(oracle.seq(kv * tk * hd, 72), oracle.seq(kv * tk * hd, 73), kv, tk, cap, hd)
+    kn, vn = kc.copy(), vc.copy()
+    kn.reshape(kv, cap, hd)[:, tk:, :] = np.nan
+    vn.reshape(kv, hd, cap)[:, :, tk:] = np.nan
+    if half:
+        run = lambda k, v: gpu.flash_attn_f16(q, up_f16(k), up_f16(v), tq, past, heads, kv, hd, cap, scale, causal)
+    else:
+        run = lambda k, v: gpu.flash_attn(q, up(k), up(v), tq, past, heads, kv, hd, cap, scale, causal)
+    a, b = run(kc, vc), run(kn, vn)
+    assert torch.isfinite(b).all() and torch.equal(a, b)
+
+
 @pytest.mark.parametrize("heads,kv,hd,causal", [(4, 2, 128, True), (4, 4, 64, False), (4, 2, 64, False),
                                                (4, 4, 128, True), (4, 4, 64, True), (4, 2, 64, True)])
 def test_fused_attention_cases(gpu, heads, kv, hd, causal):
